@@ -1,0 +1,472 @@
+#!/usr/bin/env python3
+"""WKV7 slot-pool hot path on one MI355X: decode slot-steps/s (headline),
+chunked-prefill tokens/s, 7B decode with slot forks, and a ragged mixed step.
+
+Prints ONE JSON line on stdout (progress goes to stderr):
+  value     config 1 decode slot-steps/s -- 256 active slots scattered in a
+            512-slot pool, RWKV-7 1.5B shape (H=32, 24 layers), one token per
+            slot per step through all 24 layers' WKV7 update (24 launches)
+  roofline  decode kernel: algorithmic bytes per launch / average launch
+            duration (HIP events on the launch stream) against 8 TB/s
+  cpu_baseline  the fp32 C port (oracle/, OpenMP) on this host's cores over a
+            bounded sample of the same decode workload
+
+Inputs are synthetic (wkvm_amd.synthetic distributions), generated on the GPU
+before the timed region; the per-layer input vectors (2.3 % of the bytes) are
+drawn from 4 distinct sets per layer and reused across steps, while every step
+reads and writes all 24 layers' distinct slot state (3 GiB, far beyond the
+256 MB Infinity Cache).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+BF16_DENSE_PEAK_TFLOPS = 2500.0
+
+# Algorithmic bytes (one layer, one slot): fp32 state read + write 2 x 16 KiB
+# per head, six bf16 input vectors and one bf16 y vector of 128 B per head.
+HEAD_STATE_B = 64 * 64 * 4
+HEAD_VEC_B = 64 * 2
+
+
+def slot_layer_bytes(H: int) -> int:
+    return H * (2 * HEAD_STATE_B + 7 * HEAD_VEC_B)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--prefill-iters", type=int, default=6)
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+class Launcher:
+    """Pre-bound ctypes calls into libwkv7.so (no per-call Python validation;
+    every id / shape was validated once at set-up)."""
+
+    def __init__(self, torch, dev):
+        from wkvm_amd import _lib
+
+        self.lib = _lib.load()
+        self.check = _lib.check
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def decode(self, pool, rows, H, ids, B, xs, y):
+        rc = self.lib.wkv7_decode_slots(pool, rows, H, ids, B, *xs, y, 0, 1.0, self.stream)
+        if rc:
+            self.check(rc, "wkv7_decode_slots")
+
+    def prefill(self, pool, rows, H, ids, cu, nseq, T, xs, y, zero_init, ws=None, ws_bytes=0):
+        rc = self.lib.wkv7_prefill_varlen(pool, rows, H, ids, cu, nseq, T, *xs, y, 0, zero_init,
+                                          1.0, ws, ws_bytes, self.stream)
+        if rc:
+            self.check(rc, "wkv7_prefill_varlen")
+
+    def copy(self, *args):
+        rc = self.lib.wkv7_slot_copy(*args, self.stream)
+        if rc:
+            self.check(rc, "wkv7_slot_copy")
+
+
+def ptrs(xs):
+    return [x.data_ptr() for x in xs]
+
+
+def bench_decode(torch, dev, args, launcher):
+    """Config 1: 1.5B decode, 256 of 512 slots, 24 layers."""
+    from wkvm_amd import synthetic
+
+    L, H, S, B, NSETS = 24, 32, 512, 256, 4
+    gcpu = synthetic.make_generator(args.seed)
+    ids = synthetic.active_slots(S, B, gcpu)
+    ids_t = torch.tensor(ids, dtype=torch.int32, device=dev)
+    gdev = synthetic.make_generator(args.seed + 1, dev)
+    wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
+    wkv.normal_(0.0, 0.1, generator=gdev)
+    vec_tensors = []  # kept alive for the whole run; launches use their raw pointers
+    for _ in range(L):
+        for _ in range(NSETS):
+            vec_tensors.append(synthetic.order(synthetic.wkv7_vectors((B, H, 64), gdev)))
+    vecs = [[ptrs(vec_tensors[l * NSETS + s]) for s in range(NSETS)] for l in range(L)]
+    ys = [torch.empty((B, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    pools = [wkv[l].data_ptr() for l in range(L)]
+    y_ptrs = [y.data_ptr() for y in ys]
+    idp = ids_t.data_ptr()
+
+    def step(i, events=None):
+        s = i % NSETS
+        for l in range(L):
+            if events is not None:
+                events[2 * l].record()
+            launcher.decode(pools[l], S + 1, H, idp, B, vecs[l][s], y_ptrs[l])
+            if events is not None:
+                events[2 * l + 1].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # timed region: K steps bracketed by synchronize (one rank, no barrier needed)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    # second pass of the same K steps with an event pair around every launch:
+    # the kernel's average launch duration for the roofline figure
+    per = []
+    for i in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * L)]
+        step(i, evs)
+        per.append(evs)
+    torch.cuda.synchronize()
+    durs = [evs[2 * l].elapsed_time(evs[2 * l + 1]) for evs in per for l in range(L)]
+    avg_launch_ms = sum(durs) / len(durs)
+    bytes_launch = B * slot_layer_bytes(H)
+    res = {
+        "slot_steps_per_s": B * args.steps / wall,
+        "ms_per_step": 1e3 * wall / args.steps,
+        "gpu_ms_per_step": gpu_ms / args.steps,
+        "hbm_gbps_step": B * args.steps * L * slot_layer_bytes(H) / wall / 1e9,
+        "avg_launch_us": 1e3 * avg_launch_ms,
+        "launch_gbps": bytes_launch / (avg_launch_ms * 1e-3) / 1e9,
+        "bytes_per_launch": bytes_launch,
+        "bytes_per_slot_step": L * slot_layer_bytes(H),
+        "launches": len(durs),
+    }
+    log(f"decode cfg1: {res['slot_steps_per_s']:.0f} slot-steps/s, {res['ms_per_step']:.3f} ms/step, "
+        f"launch {res['avg_launch_us']:.1f} us = {res['launch_gbps']:.0f} GB/s")
+    del wkv, vec_tensors, ys
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(torch, dev, args, launcher):
+    """Config 2: 1.5B shape, 8 sequences x 4096 tokens, zero initial state,
+    final states into 8 seeded slots; per-layer launch timing over 3 distinct
+    layers' inputs."""
+    from wkvm_amd import ops, synthetic
+
+    H, S, nseq, T, NL = 32, 16, 8, 4096, 3
+    gcpu = synthetic.make_generator(args.seed + 2)
+    ids = synthetic.active_slots(S, nseq, gcpu)
+    ids_t = torch.tensor(ids, dtype=torch.int32, device=dev)
+    cu_t = torch.arange(nseq + 1, dtype=torch.int32, device=dev) * T
+    gdev = synthetic.make_generator(args.seed + 3, dev)
+    pools = [torch.zeros((S + 1, H, 64, 64), dtype=torch.float32, device=dev) for _ in range(NL)]
+    xs = [synthetic.order(synthetic.wkv7_vectors((nseq * T, H, 64), gdev)) for _ in range(NL)]
+    ys = [torch.empty((nseq * T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(NL)]
+    ws_bytes = ops.prefill_workspace_bytes(H, nseq, nseq * T)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws_ptr = ws.data_ptr() if ws_bytes else None
+
+    def run(l):
+        launcher.prefill(pools[l].data_ptr(), S + 1, H, ids_t.data_ptr(), cu_t.data_ptr(), nseq,
+                         nseq * T, ptrs(xs[l]), ys[l].data_ptr(), 1, ws_ptr, ws_bytes)
+
+    for i in range(2):
+        run(i % NL)
+    torch.cuda.synchronize()
+    durs = []
+    t0 = time.perf_counter()
+    for i in range(args.prefill_iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run(i % NL)
+        e1.record()
+        durs.append((e0, e1))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sum(a.elapsed_time(b) for a, b in durs) / len(durs)
+    tokens = nseq * T
+    bytes_layer = tokens * H * 7 * HEAD_VEC_B + nseq * H * HEAD_STATE_B
+    flops_layer = tokens * H * (18 * 64 * 64 + 8 * 64 * 64)
+    res = {
+        "tokens_per_s_per_layer": tokens / (ms * 1e-3),
+        "ms_per_layer": ms,
+        "wall_ms_per_layer": 1e3 * wall / args.prefill_iters,
+        "hbm_gbps": bytes_layer / (ms * 1e-3) / 1e9,
+        "mfma_util": flops_layer / (ms * 1e-3) / (BF16_DENSE_PEAK_TFLOPS * 1e12),
+        "algorithmic_bytes_per_layer": bytes_layer,
+        "algorithmic_flops_per_layer": flops_layer,
+        "workspace_bytes": ws_bytes,
+        "tokens_per_s_24_layers": tokens / (ms * 1e-3) / 24,
+    }
+    log(f"prefill cfg2: {res['tokens_per_s_per_layer']:.3e} tok/s/layer, {ms:.3f} ms/layer, "
+        f"{res['hbm_gbps']:.0f} GB/s, MFMA {100 * res['mfma_util']:.2f} %")
+    del pools, xs, ys, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_fork_decode_7b(torch, dev, args, launcher):
+    """Config 3: 7B shape (H=64, 32 layers), 1024 active slots, before each of
+    10 steps fork 128 seeded live slots into the 128 free slots (wkv + shift),
+    then decode every active slot through all 32 layers."""
+    from wkvm_amd import ops, synthetic
+
+    L, H, D, S, B, NF, steps = 32, 64, 4096, 1152, 1024, 128, 10
+    gcpu = synthetic.make_generator(args.seed + 4)
+    live = synthetic.active_slots(1024, B, gcpu)
+    free = list(range(1025, S + 1))
+    gdev = synthetic.make_generator(args.seed + 5, dev)
+    wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
+    wkv.normal_(0.0, 0.1, generator=gdev)
+    shift = torch.zeros((L, 2, S + 1, D), dtype=torch.bfloat16, device=dev)
+    ids_t = torch.tensor(live, dtype=torch.int32, device=dev)
+    xs_keep = [synthetic.order(synthetic.wkv7_vectors((B, H, 64), gdev)) for _ in range(L)]
+    xs = [ptrs(x) for x in xs_keep]
+    ys = [torch.empty((B, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    srcs = []
+    for _ in range(steps + 1):
+        pick = torch.randperm(B, generator=gcpu)[:NF].tolist()
+        srcs.append(torch.tensor([live[i] for i in pick], dtype=torch.int32, device=dev))
+    dst_t = torch.tensor(free, dtype=torch.int32, device=dev)
+    w_os, w_ss, w_rows, w_rb = ops.slot_view(wkv, 1)[1:]
+    s_outer, s_os, s_ss, s_rows, s_rb = ops.slot_view(shift, 2)
+
+    def fork(i):
+        launcher.copy(wkv.data_ptr(), w_os, w_ss, w_rows, dst_t.data_ptr(), wkv.data_ptr(), w_os,
+                      w_ss, w_rows, srcs[i].data_ptr(), L, w_rb, NF)
+        launcher.copy(shift.data_ptr(), s_os, s_ss, s_rows, dst_t.data_ptr(), shift.data_ptr(),
+                      s_os, s_ss, s_rows, srcs[i].data_ptr(), s_outer, s_rb, NF)
+
+    def decode():
+        for l in range(L):
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), B, xs[l], ys[l].data_ptr())
+
+    fork(steps)
+    decode()
+    torch.cuda.synchronize()
+    fork_ms, dec_ms = [], []
+    t0 = time.perf_counter()
+    for i in range(steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        fork(i)
+        e[1].record()
+        decode()
+        e[2].record()
+        fork_ms.append((e[0], e[1]))
+        dec_ms.append((e[1], e[2]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    f_ms = sum(a.elapsed_time(b) for a, b in fork_ms) / steps
+    d_ms = sum(a.elapsed_time(b) for a, b in dec_ms) / steps
+    fork_bytes = 2 * NF * L * (H * HEAD_STATE_B + 2 * D * 2)
+    res = {
+        "slot_steps_per_s": B / (d_ms * 1e-3),
+        "decode_ms_per_step": d_ms,
+        "decode_hbm_gbps": B * L * slot_layer_bytes(H) / (d_ms * 1e-3) / 1e9,
+        "fork_ms_per_round": f_ms,
+        "fork_gbps": fork_bytes / (f_ms * 1e-3) / 1e9,
+        "fork_slots_per_s": NF / (f_ms * 1e-3),
+        "wall_ms_per_step": 1e3 * wall / steps,
+    }
+    log(f"7B fork+decode cfg3: decode {d_ms:.2f} ms/step ({res['decode_hbm_gbps']:.0f} GB/s), "
+        f"fork {f_ms:.3f} ms/round ({res['fork_gbps']:.0f} GB/s)")
+    del wkv, shift, xs_keep, ys
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_mixed(torch, dev, args, launcher):
+    """Config 4: 1.5B, 1024-slot pool; 64 rows prefill U[1, 2048] tokens from
+    zero state plus 448 rows decode one token; one decode launch and one varlen
+    prefill launch per layer, 24 layers = one scheduler step."""
+    from wkvm_amd import ops, synthetic
+
+    L, H, S, NP, ND = 24, 32, 1024, 64, 448
+    gcpu = synthetic.make_generator(args.seed + 6)
+    slots = synthetic.active_slots(S, NP + ND, gcpu)
+    pre, dec = slots[:NP], slots[NP:]
+    lens = synthetic.ragged_lengths(NP, 1, 2048, gcpu)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    T = cu[-1]
+    gdev = synthetic.make_generator(args.seed + 7, dev)
+    wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
+    wkv.normal_(0.0, 0.1, generator=gdev)
+    pre_t = torch.tensor(pre, dtype=torch.int32, device=dev)
+    dec_t = torch.tensor(dec, dtype=torch.int32, device=dev)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    dx = [synthetic.order(synthetic.wkv7_vectors((ND, H, 64), gdev)) for _ in range(L)]
+    px = [synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev)) for _ in range(2)]
+    dy = torch.empty((ND, H, 64), dtype=torch.bfloat16, device=dev)
+    py = torch.empty((T, H, 64), dtype=torch.bfloat16, device=dev)
+    ws_bytes = ops.prefill_workspace_bytes(H, NP, T)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws_ptr = ws.data_ptr() if ws_bytes else None
+
+    def step():
+        for l in range(L):
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(), ND, ptrs(dx[l]),
+                            dy.data_ptr())
+            launcher.prefill(wkv[l].data_ptr(), S + 1, H, pre_t.data_ptr(), cu_t.data_ptr(), NP, T,
+                             ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes)
+
+    step()
+    torch.cuda.synchronize()
+    reps = 3
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    step_bytes = L * (ND * slot_layer_bytes(H) + T * H * 7 * HEAD_VEC_B + NP * H * HEAD_STATE_B)
+    res = {
+        "ms_per_step": ms,
+        "prefill_tokens": T,
+        "hbm_gbps": step_bytes / (ms * 1e-3) / 1e9,
+        "tokens_per_s": (T + ND) / (ms * 1e-3),
+    }
+    log(f"mixed cfg4: {ms:.2f} ms/step over 24 layers, {T} prefill tokens + {ND} decodes, "
+        f"{res['hbm_gbps']:.0f} GB/s")
+    del wkv, dx, px, dy, py, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(args):
+    """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
+    slots of a 512-slot pool) for as many steps as fit ~10 s, at least one."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    from wkvm_amd import synthetic
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    O.set_threads(threads)
+    L, H, S, B = 24, 32, 512, 256
+    gen = synthetic.make_generator(args.seed)
+    ids = synthetic.active_slots(S, B, gen)
+    pool = np.zeros((L, S + 1, H, 64, 64), dtype=np.float32)
+    for l in range(L):
+        pool[l, ids] = 0.01
+    vecs = [synthetic.wkv7_vectors((B, H, 64), gen) for _ in range(L)]
+    bits = [[v[n].contiguous().view(torch.int16).numpy().view(np.uint16) for n in "rwkvab"]
+            for v in vecs]
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        for l in range(L):
+            O.port_decode_slots_f32(pool[l], ids, *bits[l])
+        steps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or steps >= 20:
+            break
+    res = {
+        "value": B * steps / el,
+        "unit": "slot-steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} config-1 decode steps (24 layers x 256 slots, H=32), fp32 C port "
+                  f"with OpenMP, {el:.1f} s",
+    }
+    log(f"cpu baseline: {res['value']:.1f} slot-steps/s on {threads} threads ({steps} steps)")
+    return res
+
+
+def pmc_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary,
+    if present (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel)."""
+    path = os.path.join(ROOT, "profiles", "decode_cfg1_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the WKV7 slot-pool path shards by slot with no "
+              "exchange step, and this build runs on a single MI355X (see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    launcher = Launcher(torch, dev)
+    dec = bench_decode(torch, dev, args, launcher)
+    pre = bench_prefill(torch, dev, args, launcher)
+    extra = {}
+    if not args.no_extra:
+        extra["fork_decode_7b"] = bench_fork_decode_7b(torch, dev, args, launcher)
+        extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args)
+    line = {
+        "metric": "WKV7 decode slot-steps/s + achieved HBM GB/s; chunked-prefill tokens/s",
+        "value": round(dec["slot_steps_per_s"], 1),
+        "unit": "slot-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 state / bf16 vectors",
+        "data": "synthetic (seeded; BASELINE input distributions)",
+        "config": {
+            "workload": "config 1: WKV7 decode, RWKV-7 1.5B shape (H=32, N=64, 24 layers), "
+                        "256 active slots scattered in a 512-slot fp32 pool, 1 token/slot/step",
+            "slots": 256, "pool": 512, "layers": 24, "heads": 32, "head_size": 64,
+            "parallelism": "single GPU",
+        },
+        "hbm_gbps": round(dec["hbm_gbps_step"], 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dec["launch_gbps"], 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec["launch_gbps"] / HBM_PEAK_GBPS, 4),
+            "traffic": pmc_traffic(),
+            "kernel": "decode_slots_kernel",
+            "bytes_per_launch": dec["bytes_per_launch"],
+            "avg_launch_us": round(dec["avg_launch_us"], 2),
+        },
+        "decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()},
+        "prefill": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in pre.items()},
+        **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+           for k, v in extra.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,157 @@
+/*
+ * wkv7.h -- C ABI of the MI355X (gfx950) WKV7 slot-pool library, libwkv7.so.
+ *
+ * The reference (xiaol/wkvm) is pure Python: it keeps request state in a
+ * layer-major slot pool (wkvm/runner/state.py:35-46) and runs the WKV7
+ * recurrence through the third-party `fla` package's Triton kernels
+ * (wkvm/models/rwkv7.py:108-113) between gather/scatter copies of the pool.
+ * Each entry point below replaces one of those operations; the comment on each
+ * names the reference code it stands in for. The Python host package
+ * `wkvm_amd` binds these symbols with ctypes; INTEGRATION.md shows the
+ * binding a maintainer would add to the reference.
+ *
+ * Conventions (all entry points):
+ *  - Memory: every pointer is caller-owned device memory (except where a
+ *    parameter says "host"). The library never allocates, frees or
+ *    synchronises; work is enqueued on `stream` (a hipStream_t, or NULL for
+ *    the default stream) and is asynchronous to the host.
+ *  - Slot pool layout (wkvm/runner/state.py:35-46): one layer of the wkv
+ *    family is a contiguous fp32 tensor [num_rows, H, 64, 64] with
+ *    num_rows = num_slots + 1 (row 0 is the reserved pad slot,
+ *    wkvm/core/arena.py:32-37). Element [row, h, j, i] is the state entry for
+ *    key index j and value index i (h = S^T of S_t = S_{t-1} diag(w) + ...).
+ *  - Per-token vectors r, w, k, v, a, b are bf16 (passed as uint16_t bit
+ *    patterns), contiguous [tokens, H, 64]. `w` is LOG-decay: the
+ *    multiplicative decay applied to the state is exp(w), computed in fp32.
+ *    This is the convention of the fla wkv op the reference calls.
+ *  - Recurrence, per token and head (fp32 arithmetic):
+ *        p_i     = sum_j a[j] h[j][i]
+ *        h[j][i] = exp(w[j]) h[j][i] + b[j] p_i + k[j] v[i]
+ *        y[i]    = sum_j (scale r[j]) h[j][i]
+ *  - Slot ids are int32 in device memory. A kernel never touches memory
+ *    outside [0, num_rows): rows whose id is out of range are skipped. Host
+ *    wrappers validate ids before launch and raise instead.
+ *  - Return value: 0 on success, a negative WKV7_ERR_* code for rejected
+ *    arguments (nothing is enqueued), or a positive hipError_t from the launch.
+ *  - Thread safety: calls are stream-ordered; two calls that write the same
+ *    slot rows on different streams race.
+ */
+#ifndef WKV7_H
+#define WKV7_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WKV7_ABI_VERSION 1
+
+#define WKV7_OK 0
+#define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
+#define WKV7_ERR_SHAPE (-2)     /* head size other than 64, misaligned rows */
+#define WKV7_ERR_WORKSPACE (-3) /* workspace missing or too small */
+
+#define WKV7_Y_BF16 0 /* y written as bf16 (round to nearest even) */
+#define WKV7_Y_F32 1  /* y written as fp32 */
+
+/* ABI version of the loaded library (WKV7_ABI_VERSION at build time). */
+int wkv7_abi_version(void);
+
+/* Human-readable text for a return code (WKV7_ERR_* or hipError_t). */
+const char *wkv7_strerror(int code);
+
+/*
+ * One decode step (one token per slot) for B slots of one layer, in place.
+ *
+ * Replaces, per layer of RWKV7Runner.decode_step (wkvm/runner/runner.py:65-89):
+ * the `index_select` gather of the batch's wkv rows
+ * (wkvm/runner/state.py:77), fla's fused recurrent WKV7 kernel on the gathered
+ * [B, H, K, V] state (dispatched for seq_len < 64, wkvm/models/rwkv7.py:110-111),
+ * and the `index_copy_` scatter back (wkvm/runner/state.py:91). State is read
+ * and written at its slot row; nothing is gathered.
+ *
+ *   wkv_layer  [num_rows, H, 64, 64] fp32, updated in place at rows slot_ids[b]
+ *   slot_ids   [B] int32 (device); must be distinct (duplicates race)
+ *   r..b       [B, H, 64] bf16
+ *   y          [B, H, 64], dtype per y_dtype (WKV7_Y_BF16 | WKV7_Y_F32)
+ */
+int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
+                      const int32_t *slot_ids, int32_t B,
+                      const uint16_t *r, const uint16_t *w, const uint16_t *k,
+                      const uint16_t *v, const uint16_t *a, const uint16_t *b,
+                      void *y, int32_t y_dtype, float scale, void *stream);
+
+/*
+ * Chunked prefill of nseq ragged sequences of one layer; each sequence starts
+ * from its slot's state (or from zero when zero_init != 0) and leaves its
+ * final state in that slot.
+ *
+ * Replaces, per layer, fla's `chunk_rwkv7` (chunk 64) and its fused recurrent
+ * tail as called by RWKV7Runner.prefill (wkvm/runner/runner.py:41-63, one
+ * request per call from Engine._execute, wkvm/engine.py:152-155), together
+ * with the per-chunk gather/scatter round trip through the bank
+ * (wkvm/runner/state.py:63-97). Ragged batching follows the cu_seqlens
+ * (q_start_loc) contract of MixedBatchMetadata (wkvm/core/mixed_batch.py:213-270).
+ *
+ *   wkv_layer     [num_rows, H, 64, 64] fp32
+ *   slot_ids      [nseq] int32 (device), distinct
+ *   cu_seqlens    [nseq + 1] int32 (device), cu_seqlens[0] = 0,
+ *                 non-decreasing, cu_seqlens[nseq] = total_tokens
+ *   r..b          [total_tokens, H, 64] bf16
+ *   y             [total_tokens, H, 64], dtype per y_dtype
+ *   workspace     device scratch of at least
+ *                 wkv7_prefill_workspace_bytes(H, nseq, total_tokens) bytes
+ *                 (may be NULL when that size is 0)
+ */
+int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
+                        const int32_t *slot_ids, const int32_t *cu_seqlens,
+                        int32_t nseq, int64_t total_tokens,
+                        const uint16_t *r, const uint16_t *w, const uint16_t *k,
+                        const uint16_t *v, const uint16_t *a, const uint16_t *b,
+                        void *y, int32_t y_dtype, int32_t zero_init, float scale,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* Scratch bytes wkv7_prefill_varlen needs for this problem size. */
+size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t total_tokens);
+
+/*
+ * Copy slot rows between two slot-indexed tensors (or within one), bit-exact.
+ *
+ * A tensor here is `outer` blocks of `rows` slot rows; each slot row is
+ * `row_bytes` contiguous bytes. Pair p copies, for every outer block o,
+ *     src + o*src_outer_stride + src_ids[p]*src_slot_stride   (row_bytes)
+ *  -> dst + o*dst_outer_stride + dst_ids[p]*dst_slot_stride.
+ * A NULL id array means the identity (ids 0..n-1). Strides are in bytes.
+ *
+ * Replaces: the snapshot/restore slot-view copies of StateStore.save/load
+ * (`bank.wkv[:, slot]`, `bank.shift[:, :, slot]`, wkvm/store.py:130-131 and
+ * 151-152) as a device-to-device fork; the O(MB) copy StateArena.fork leaves
+ * to the runner (wkvm/core/arena.py:82-93); and the per-layer
+ * `index_select` / `index_copy_` of RWKV7StateBank.gather_cache /
+ * scatter_cache (wkvm/runner/state.py:63-97), for which src (gather) or dst
+ * (scatter) is a dense staging tensor with NULL ids.
+ * Precondition: no dst row is written twice and no dst row is also a src row
+ * (sources are not snapshotted first); duplicate src ids are allowed.
+ */
+int wkv7_slot_copy(void *dst, int64_t dst_outer_stride, int64_t dst_slot_stride,
+                   int64_t dst_rows, const int32_t *dst_ids,
+                   const void *src, int64_t src_outer_stride, int64_t src_slot_stride,
+                   int64_t src_rows, const int32_t *src_ids,
+                   int64_t outer, int64_t row_bytes, int32_t n, void *stream);
+
+/*
+ * Zero slot rows (admission reset: zero state == empty prefix).
+ * Replaces RWKV7StateBank.zero_slots (wkvm/runner/state.py:50-54). Uses a fill
+ * kernel, not a memset node, so it is safe inside captured HIP graphs.
+ */
+int wkv7_slot_zero(void *base, int64_t outer_stride, int64_t slot_stride, int64_t rows,
+                   const int32_t *ids, int64_t outer, int64_t row_bytes, int32_t n,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WKV7_H */

@@ -1,0 +1,172 @@
+"""Decode-step parity: wkv7_decode_slots (HIP, through the C ABI) against the
+float64 oracle on the same seeded inputs.
+
+Bars (north star): the fp32 state matches to max relative error 1e-5 per step,
+measured normwise per (slot, head) 64x64 tile as max|d| / max|ref|; y in fp32
+matches to the same bar per (slot, head) vector; y in bf16 is within one bf16
+ulp of the float64 result rounded to bf16. Rows not in the batch, including
+pad slot 0, stay bit-identical."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from tests import util as U
+from tests.golden import make_golden as G
+from wkvm_amd import ops, synthetic
+from wkvm_amd.layout import RWKV7StateLayout
+from wkvm_amd.runner import WKV7Runner
+from wkvm_amd.state import RWKV7StateBank
+
+pytestmark = pytest.mark.gpu
+
+STATE_TOL = 1e-5
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "wkv7_golden.npz")
+
+
+def _check_step(pool_before: np.ndarray, ids, vec_bits, pool_after: torch.Tensor, y: torch.Tensor,
+                scale: float = 1.0):
+    y_ref, h_ref = O.scan_bf16(np.arange(len(ids) + 1), *vec_bits, pool=pool_before,
+                               slot_ids=ids, scale=scale)
+    h = U.f64(pool_after[ids])
+    err = U.normwise_max(h, h_ref)
+    assert err <= STATE_TOL, f"state normwise error {err:.3e}"
+    if y.dtype == torch.float32:
+        yerr = U.normwise_max(U.f64(y), y_ref, tile_dims=1)
+        assert yerr <= STATE_TOL, f"y normwise error {yerr:.3e}"
+    else:
+        ulps = U.bf16_ulp_distance(U.bits(y), y_ref)
+        assert ulps.max() <= 1, f"y off by {ulps.max()} bf16 ulps"
+    return err
+
+
+@pytest.mark.parametrize("y_dtype", [torch.bfloat16, torch.float32])
+def test_cfg0_decode_matches_oracle_and_golden(dev, y_dtype):
+    pool, ids, vecs = G.cfg0_inputs()
+    gpool = pool.to(dev)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    y = ops.wkv7_decode_slots(gpool, ids, *xs, out_dtype=y_dtype)
+    torch.cuda.synchronize()
+    _check_step(pool.numpy(), ids, U.vec_bits(vecs), gpool, y)
+    others = [i for i in range(pool.shape[0]) if i not in ids]
+    assert torch.equal(gpool[others].cpu(), pool[others]), "rows outside the batch changed"
+    g = np.load(GOLDEN)
+    if y_dtype == torch.float32:
+        assert U.normwise_max(U.f64(y), g["cfg0_y"], tile_dims=1) <= STATE_TOL
+    h = U.f64(gpool[ids])
+    assert U.normwise_max(h @ G.projection_vector(), g["cfg0_state_proj"], 1) <= 1e-4
+    assert U.normwise_max(h[0, 0], g["cfg0_state_block"]) <= STATE_TOL
+
+
+def test_cfg1_full_layer_multi_step(dev):
+    """1.5B shape (H=32), 256 active slots scattered in a 512-slot pool, three
+    consecutive steps; each step is checked against the oracle run from the
+    GPU's own previous state (per-step bar), and the 3-step drift against an
+    oracle chain is reported."""
+    H, S, B = 32, 512, 256
+    gen = synthetic.make_generator(101)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = synthetic.active_slots(S, B, gen)
+    gpool = pool.to(dev)
+    chain = pool.numpy().astype(np.float64)
+    for step in range(3):
+        vecs = synthetic.wkv7_vectors((B, H, 64), gen)
+        before = gpool.cpu().numpy()
+        y = ops.wkv7_decode_slots(gpool, ids, *(vecs[n].to(dev) for n in "rwkvab"),
+                                  out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        err = _check_step(before, ids, U.vec_bits(vecs), gpool, y)
+        _, chain_h = O.scan_f64(np.arange(B + 1), *(O.bf16_bits_to_f64(b) for b in U.vec_bits(vecs)),
+                                h0=chain[ids])
+        chain[ids] = chain_h
+        print(f"step {step}: per-step normwise {err:.2e}, "
+              f"drift vs f64 chain {U.normwise_max(U.f64(gpool[ids]), chain[ids]):.2e}")
+    untouched = [i for i in range(S + 1) if i not in set(ids)]
+    assert torch.equal(gpool[untouched].cpu(), pool[untouched])
+
+
+def test_delta_rule_orientation_on_gpu(dev):
+    """CF3 through the kernel: decay 1, a = -k^, b = k^ (bf16), k = k^:
+    S_1 k^ = (1 - k^.k^) S_0 k^ + (k^.k^) v in exact arithmetic with the bf16
+    vectors; a transposed kernel misses this for a non-symmetric S_0."""
+    H = 8
+    g = torch.Generator().manual_seed(12)
+    kh = torch.nn.functional.normalize(torch.randn((1, H, 64), generator=g), dim=-1).bfloat16()
+    v = torch.randn((1, H, 64), generator=g).bfloat16()
+    r = torch.randn((1, H, 64), generator=g).bfloat16()
+    zero = torch.zeros((1, H, 64), dtype=torch.bfloat16)
+    pool = torch.randn((2, H, 64, 64), generator=g)
+    gpool = pool.to(dev)
+    ops.wkv7_decode_slots(gpool, [1], *(x.to(dev) for x in (r, zero, kh, v, -kh, kh)))
+    k64 = kh.double().numpy()[0]
+    kk = np.sum(k64 * k64, -1)[:, None]
+    S0k = np.einsum("hji,hj->hi", pool.double().numpy()[1], k64)
+    S1k = np.einsum("hji,hj->hi", U.f64(gpool[1]), k64)
+    expect = (1 - kk) * S0k + kk * v.double().numpy()[0]
+    assert np.max(np.abs(S1k - expect)) <= 1e-4 * np.max(np.abs(expect))
+
+
+def test_permutation_equivariance_and_scale(dev):
+    """CF7: the same rows in another batch order give identical bits; scale
+    multiplies r, so y(scale=0.5) == 0.5 * y(scale=1) exactly in fp32."""
+    H, S = 4, 12
+    gen = synthetic.make_generator(13)
+    base = synthetic.initial_states((S + 1, H, 64, 64), gen).to(dev)
+    ids = [3, 9, 1, 12, 6]
+    vecs = synthetic.wkv7_vectors((5, H, 64), gen, device=dev)
+    perm = [2, 0, 4, 1, 3]
+    p1, p2, p3 = base.clone(), base.clone(), base.clone()
+    y1 = ops.wkv7_decode_slots(p1, ids, *synthetic.order(vecs), out_dtype=torch.float32)
+    y2 = ops.wkv7_decode_slots(p2, [ids[i] for i in perm],
+                               *(vecs[n][perm] for n in "rwkvab"), out_dtype=torch.float32)
+    assert torch.equal(p1, p2)
+    assert torch.equal(y1[perm], y2)
+    y3 = ops.wkv7_decode_slots(p3, ids, *synthetic.order(vecs), scale=0.5, out_dtype=torch.float32)
+    assert torch.equal(p3, p1)
+    assert torch.equal(y3, y1 * 0.5)
+
+
+def test_decode_argument_errors(dev):
+    pool = torch.zeros((5, 2, 64, 64), device=dev)
+    vecs = synthetic.order(synthetic.wkv7_vectors((2, 2, 64), synthetic.make_generator(0),
+                                                  device=dev))
+    with pytest.raises(ValueError, match="duplicate"):
+        ops.wkv7_decode_slots(pool, [1, 1], *vecs)
+    with pytest.raises(ValueError, match="out of range"):
+        ops.wkv7_decode_slots(pool, [1, 5], *vecs)
+    with pytest.raises(ValueError, match="bfloat16"):
+        ops.wkv7_decode_slots(pool, [1, 2], *(x.float() for x in vecs))
+    with pytest.raises(ValueError):
+        ops.wkv7_decode_slots(pool, [1, 2, 3], *vecs)
+    with pytest.raises(ValueError):
+        ops.wkv7_decode_slots(pool.double(), [1, 2], *vecs)
+    y = ops.wkv7_decode_slots(pool, [], *(x[:0] for x in vecs))
+    assert y.shape == (0, 2, 64)
+
+
+def test_runner_decode_step_all_layers(dev):
+    """WKV7Runner.decode_step over a 4-layer bank equals per-layer oracle steps;
+    the pad slot and idle slots stay untouched."""
+    lay = RWKV7StateLayout(n_layer=4, hidden_size=384, num_heads=6, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    bank = RWKV7StateBank(lay, num_slots=10, device=dev)
+    gen = synthetic.make_generator(21)
+    bank.wkv[:, 1:] = synthetic.initial_states((4, 10, 6, 64, 64), gen).to(dev)
+    before = bank.wkv.cpu().numpy()
+    batch = [{"wkv": s, "shift": s} for s in (4, 2, 9)]
+    layer_vecs = [synthetic.wkv7_vectors((3, 6, 64), gen) for _ in range(4)]
+    run = WKV7Runner(bank)
+    ys = run.decode_step(batch, [[v[n].to(dev) for n in "rwkvab"] for v in layer_vecs],
+                         out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for layer in range(4):
+        _check_step(before[layer], [4, 2, 9], U.vec_bits(layer_vecs[layer]), bank.wkv[layer],
+                    ys[layer])
+    idle = [0, 1, 3, 5, 6, 7, 8, 10]
+    assert np.array_equal(bank.wkv[:, idle].cpu().numpy(), before[:, idle])

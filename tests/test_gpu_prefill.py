@@ -1,0 +1,196 @@
+"""Prefill parity: wkv7_prefill_varlen (HIP, through the C ABI) against the
+float64 oracle on the same seeded inputs.
+
+Bars (north star): relative L2 <= 1e-3 per sequence on the final state and on
+the per-token y. A bf16 y is compared with the float64 y rounded to bf16 (the
+rounding of the output alone is ~1.5e-3 relative L2, so comparing it with the
+unrounded value would test the storage format, not the kernel); an fp32 y is
+compared with the unrounded value."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from tests import util as U
+from wkvm_amd import ops, synthetic
+from wkvm_amd.layout import RWKV7StateLayout
+from wkvm_amd.runner import WKV7Runner
+from wkvm_amd.state import RWKV7StateBank
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+
+
+def _check(pool_before, ids, cu, vbits, gpool, y, zero_init, tol=REL_L2):
+    y_ref, h_ref = O.scan_bf16(cu, *vbits, pool=None if zero_init else pool_before,
+                               slot_ids=None if zero_init else ids)
+    h = U.f64(gpool[ids])
+    yv = U.f64(y)
+    if y.dtype == torch.bfloat16:
+        y_cmp = O.round_f64_to_bf16(y_ref)
+    else:
+        y_cmp = y_ref
+    worst_h, worst_y = 0.0, 0.0
+    for s in range(len(ids)):
+        worst_h = max(worst_h, U.rel_l2(h[s], h_ref[s]))
+        if cu[s + 1] > cu[s]:
+            worst_y = max(worst_y, U.rel_l2(yv[cu[s]:cu[s + 1]], y_cmp[cu[s]:cu[s + 1]]))
+    assert worst_h <= tol, f"final state rel L2 {worst_h:.3e}"
+    assert worst_y <= tol, f"y rel L2 {worst_y:.3e}"
+    return worst_h, worst_y
+
+
+@pytest.mark.parametrize("zero_init", [False, True])
+@pytest.mark.parametrize("y_dtype", [torch.bfloat16, torch.float32])
+def test_ragged_lengths_from_slot_state(dev, zero_init, y_dtype):
+    """Edge lengths around the chunk size, a zero-length and a length-1 row."""
+    H, S = 4, 12
+    lens = [1, 5, 0, 63, 64, 65, 130, 257]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    gen = synthetic.make_generator(31)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = synthetic.active_slots(S, len(lens), gen)
+    vecs = synthetic.wkv7_vectors((int(cu[-1]), H, 64), gen)
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_varlen(gpool, ids, cu.tolist(), *(vecs[n].to(dev) for n in "rwkvab"),
+                                zero_init=zero_init, out_dtype=y_dtype)
+    torch.cuda.synchronize()
+    _check(pool.numpy(), ids, cu, U.vec_bits(vecs), gpool, y, zero_init)
+    others = [i for i in range(S + 1) if i not in ids]
+    assert torch.equal(gpool[others].cpu(), pool[others])
+    if zero_init:  # the zero-length row leaves an all-zero (fresh) state
+        assert gpool[ids[2]].abs().sum().item() == 0.0
+    else:          # ... or its slot state untouched
+        assert torch.equal(gpool[ids[2]].cpu(), pool[ids[2]])
+
+
+def test_cfg2_full_size_zero_init(dev):
+    """Config 2: 1.5B shape (H=32), 8 sequences x 4096 tokens from zero state,
+    final states written to 8 seeded slots of a 16-slot pool; every token's y
+    and every final state checked."""
+    H, S, nseq, T = 32, 16, 8, 4096
+    gen = synthetic.make_generator(2)
+    ids = synthetic.active_slots(S, nseq, gen)
+    vecs = synthetic.wkv7_vectors((nseq * T, H, 64), gen)
+    cu = np.arange(nseq + 1) * T
+    gpool = torch.full((S + 1, H, 64, 64), 7.0, device=dev)  # stale contents must be ignored
+    y = ops.wkv7_prefill_varlen(gpool, ids, cu.tolist(), *(vecs[n].to(dev) for n in "rwkvab"),
+                                zero_init=True)
+    torch.cuda.synchronize()
+    eh, ey = _check(None, ids, cu, U.vec_bits(vecs), gpool, y, zero_init=True)
+    print(f"cfg2: worst final-state rel L2 {eh:.2e}, worst y rel L2 (bf16) {ey:.2e}")
+    others = [i for i in range(S + 1) if i not in ids]
+    assert bool((gpool[others] == 7.0).all())
+
+
+def test_chunk_split_invariance_through_the_slot(dev):
+    """CF6: one call over T tokens equals the runner's chunked re-entry through
+    the slot (prefill_chunk 64, 100 and 4096), as a preempted request's would."""
+    lay = RWKV7StateLayout(n_layer=2, hidden_size=512, num_heads=8, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    T = 700
+    gen = synthetic.make_generator(41)
+    layer_vecs = [synthetic.wkv7_vectors((T, 8, 64), gen, device=dev) for _ in range(2)]
+    inputs = [synthetic.order(v) for v in layer_vecs]
+    finals, outs = [], []
+    for chunk in (4096, 64, 100):
+        bank = RWKV7StateBank(lay, num_slots=3, device=dev)
+        run = WKV7Runner(bank, prefill_chunk=chunk)
+        ys = run.prefill(inputs, {"wkv": 2, "shift": 2}, out_dtype=torch.float32)
+        finals.append(bank.wkv[:, 2].clone())
+        outs.append(torch.stack(ys))
+    for f, o in zip(finals[1:], outs[1:]):
+        assert U.rel_l2(U.f64(f), U.f64(finals[0])) <= 1e-5
+        assert U.rel_l2(U.f64(o), U.f64(outs[0])) <= 1e-5
+
+
+def test_fla_signatures(dev):
+    """chunk_rwkv7 / fused_recurrent_rwkv7 with [B, T, H, K] tensors, an initial
+    state, packed cu_seqlens and head_first, against the oracle."""
+    B, T, H = 3, 80, 4
+    gen = synthetic.make_generator(51)
+    vecs = synthetic.wkv7_vectors((B, T, H, 64), gen)
+    h0 = synthetic.initial_states((B, H, 64, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    h0d = h0.to(dev)
+    o, hT = ops.chunk_rwkv7(*xs, scale=1.0, initial_state=h0d, output_final_state=True)
+    flat_bits = [U.bits(vecs[n].reshape(B * T, H, 64)) for n in "rwkvab"]
+    cu = np.arange(B + 1) * T
+    y_ref, h_ref = O.scan_bf16(cu, *flat_bits, pool=h0.numpy(), slot_ids=list(range(B)))
+    assert o.shape == (B, T, H, 64) and o.dtype == torch.bfloat16
+    assert U.rel_l2(U.f64(hT), h_ref) <= REL_L2
+    assert U.rel_l2(U.f64(o).reshape(B * T, H, 64), O.round_f64_to_bf16(y_ref)) <= REL_L2
+    assert torch.equal(h0d.cpu(), h0)  # the caller's initial_state is not modified
+    o2, h2 = ops.fused_recurrent_rwkv7(*(x.transpose(1, 2) for x in xs), initial_state=h0.to(dev),
+                                       head_first=True)
+    assert torch.equal(o2.transpose(1, 2), o) and torch.equal(h2, hT)
+    # packed sequences of lengths 30, 0, 120 with no initial state
+    lens = [30, 0, 120]
+    packed = synthetic.wkv7_vectors((1, sum(lens), H, 64), gen)
+    cu = [0, 30, 30, 150]
+    o3, h3 = ops.chunk_rwkv7(*(packed[n].to(dev) for n in "rwkvab"), cu_seqlens=cu)
+    y_ref, h_ref = O.scan_bf16(np.array(cu), *(U.bits(packed[n][0]) for n in "rwkvab"))
+    assert U.rel_l2(U.f64(h3), h_ref) <= REL_L2
+    assert U.rel_l2(U.f64(o3[0]), O.round_f64_to_bf16(y_ref)) <= REL_L2
+    assert h3[1].abs().sum().item() == 0.0
+    _, none = ops.chunk_rwkv7(*xs, output_final_state=False)
+    assert none is None
+
+
+def test_prefill_argument_errors(dev):
+    pool = torch.zeros((5, 2, 64, 64), device=dev)
+    vecs = synthetic.order(synthetic.wkv7_vectors((10, 2, 64), synthetic.make_generator(0),
+                                                  device=dev))
+    with pytest.raises(ValueError):
+        ops.wkv7_prefill_varlen(pool, [1, 2], [0, 4, 9], *vecs)        # does not end at T
+    with pytest.raises(ValueError):
+        ops.wkv7_prefill_varlen(pool, [1, 2], [0, 6, 4, 10], *vecs)   # wrong count
+    with pytest.raises(ValueError, match="duplicate"):
+        ops.wkv7_prefill_varlen(pool, [1, 1], [0, 4, 10], *vecs)
+    with pytest.raises(ValueError, match="bfloat16"):
+        ops.wkv7_prefill_varlen(pool, [1, 2], [0, 4, 10], *(x.float() for x in vecs))
+
+
+def test_mixed_step_equals_separate_calls(dev):
+    """Config 4's shape at reduced size: one decode launch + one varlen prefill
+    launch per layer equals running every row on its own (the reference
+    engine's own decomposition, wkvm/engine.py:142-170)."""
+    lay = RWKV7StateLayout(n_layer=2, hidden_size=256, num_heads=4, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    gen = synthetic.make_generator(61)
+    S = 20
+    init = synthetic.initial_states((2, S + 1, 4, 64, 64), gen).to(dev)
+    dec_slots = [3, 7, 11, 15, 19]
+    pre_slots = [1, 9, 18]
+    lens = [1, 97, 200]
+    dec_in = [synthetic.order(synthetic.wkv7_vectors((5, 4, 64), gen, device=dev)) for _ in range(2)]
+    pre_in = [synthetic.order(synthetic.wkv7_vectors((sum(lens), 4, 64), gen, device=dev))
+              for _ in range(2)]
+    bank = RWKV7StateBank(lay, num_slots=S, device=dev)
+    bank.wkv.copy_(init)
+    run = WKV7Runner(bank)
+    dys, pys = run.mixed_step([{"wkv": s, "shift": s} for s in dec_slots], dec_in,
+                              [{"wkv": s, "shift": s} for s in pre_slots], lens, pre_in,
+                              out_dtype=torch.float32)
+    ref = RWKV7StateBank(lay, num_slots=S, device=dev)
+    ref.wkv.copy_(init)
+    cu = [0, 1, 98, 298]
+    for layer in range(2):
+        for i, s in enumerate(dec_slots):
+            y = ref.decode_wkv(layer, [{"wkv": s, "shift": s}], *(x[i:i + 1] for x in dec_in[layer]),
+                               out_dtype=torch.float32)
+            assert torch.equal(y, dys[layer][i:i + 1])
+        for i, s in enumerate(pre_slots):
+            y = ref.prefill_wkv(layer, [{"wkv": s, "shift": s}], [0, lens[i]],
+                                *(x[cu[i]:cu[i + 1]] for x in pre_in[layer]),
+                                out_dtype=torch.float32)
+            assert U.rel_l2(U.f64(y), U.f64(pys[layer][cu[i]:cu[i + 1]])) <= 1e-6
+    assert U.rel_l2(U.f64(bank.wkv), U.f64(ref.wkv)) <= 1e-6
+    with pytest.raises(ValueError, match="same step"):
+        run.mixed_step([{"wkv": 1, "shift": 1}], [[x[:1] for x in d] for d in dec_in],
+                       [{"wkv": 1, "shift": 1}], [1], [[x[:1] for x in p] for p in pre_in])

@@ -1,0 +1,197 @@
+"""Host-side logic, no GPU: layout bytes, C-ABI symbol table and argument
+rejection, Python validation, and that nothing silently falls back to CPU."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from wkvm_amd import _lib, ops, synthetic
+from wkvm_amd.layout import ModelStateSpec, RWKV7StateLayout, StateFamilySpec
+from wkvm_amd.runner import WKV7Runner
+
+
+# -- layout (wkvm/models/rwkv7.py:41-99) ---------------------------------------------------
+
+@pytest.mark.parametrize("name,wkv_bytes,shift_bytes", [
+    ("0.1B", 12 * 12 * 64 * 64 * 4, 12 * 2 * 768 * 2),
+    ("1.5B", 12_582_912, 196_608),          # 12.19 MiB per slot (m2_engine_bench.md:9)
+    ("7B", 33_554_432, 524_288),
+])
+def test_layout_bytes(name, wkv_bytes, shift_bytes):
+    lay = RWKV7StateLayout.for_shape(name)
+    spec = lay.state_spec()
+    fam = {f.name: f for f in spec.families}
+    assert fam["wkv"].bytes_per_slot == wkv_bytes
+    assert fam["shift"].bytes_per_slot == shift_bytes
+    assert spec.bytes_per_request == wkv_bytes + shift_bytes
+    assert fam["wkv"].layer_ids == tuple(range(lay.n_layer))
+    assert lay.wkv_shape == (lay.num_heads, 64, 64)
+    assert lay.shift_shape == (lay.hidden_size,)
+
+
+def test_layout_from_config_mirrors_reference():
+    class Cfg:
+        num_hidden_layers = 12
+        hidden_size = 768
+        num_heads = 12
+        head_dim = 64
+        value_dim = [768] * 12
+        attn = None
+
+    lay = RWKV7StateLayout.from_config(Cfg, dtype=torch.bfloat16)
+    assert lay == RWKV7StateLayout.for_shape("0.1B")
+    Cfg.value_dim = [768, 512]
+    with pytest.raises(NotImplementedError):
+        RWKV7StateLayout.from_config(Cfg, dtype=torch.bfloat16)
+
+
+def test_spec_validation():
+    with pytest.raises(ValueError):
+        StateFamilySpec(name="wkv", bytes_per_slot=0)
+    f = StateFamilySpec(name="wkv", bytes_per_slot=4)
+    with pytest.raises(ValueError):
+        ModelStateSpec(families=(f, f))
+
+
+# -- C ABI ---------------------------------------------------------------------------------
+
+def test_header_declares_exactly_the_bound_symbols():
+    declared = set(_lib.header_symbols())
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    lib = _lib.load()
+    for name in _lib.header_symbols():
+        assert hasattr(lib, name), name
+    assert lib.wkv7_abi_version() == 1
+
+
+def test_abi_rejects_bad_arguments_before_any_launch():
+    """Every rejection returns before touching the GPU, so it runs on CPU."""
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)
+    six = [dummy] * 6
+    # decode: negative B, bad y dtype, null pool
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, -1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, 1, *six, dummy, 7, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(None, 5, 2, dummy, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 0, dummy, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, 0, *six, dummy, 0, 1.0, None) == _lib.WKV7_OK
+    # prefill: negative sizes, missing cu_seqlens
+    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, dummy, -1, 0, *six, dummy, 0, 0, 1.0,
+                                   None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, None, 1, 4, *six, dummy, 0, 0, 1.0,
+                                   None, 0, None) == _lib.WKV7_ERR_ARG
+    # slot copy: negative count, null src, row wider than the slot stride
+    assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, dummy, 0, 64, 4, None, 1, 64, -1,
+                              None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, None, 0, 64, 4, None, 1, 64, 1,
+                              None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, dummy, 0, 32, 4, None, 1, 64, 1,
+                              None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_slot_zero(None, 0, 64, 4, dummy, 1, 64, 1, None) == _lib.WKV7_ERR_ARG
+    for code in (_lib.WKV7_ERR_ARG, _lib.WKV7_ERR_SHAPE, _lib.WKV7_ERR_WORKSPACE):
+        assert _lib.strerror(code)
+
+
+def test_check_maps_codes_to_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.WKV7_ERR_ARG, "x")
+    _lib.check(_lib.WKV7_OK, "x")
+
+
+# -- Python validation / no CPU fallback ------------------------------------------------------
+
+def _vecs(B, H):
+    g = synthetic.make_generator(0)
+    return synthetic.order(synthetic.wkv7_vectors((B, H, 64), g))
+
+
+def test_ops_refuse_cpu_tensors():
+    pool = torch.zeros((4, 2, 64, 64))
+    with pytest.raises(ValueError, match="GPU"):
+        ops.wkv7_decode_slots(pool, [1, 2], *_vecs(2, 2))
+    with pytest.raises(ValueError, match="GPU"):
+        ops.wkv7_prefill_varlen(pool, [1], [0, 2], *_vecs(2, 2))
+    with pytest.raises(ValueError, match="GPU"):
+        ops.slot_copy(pool, [1], pool, [2], slot_dim=0)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.chunk_rwkv7(*(x[None] for x in _vecs(3, 2)))
+
+
+def test_host_id_validation():
+    assert ops.host_ids([3, 1], 4, "ids", distinct=True) == [3, 1]
+    with pytest.raises(ValueError, match="out of range"):
+        ops.host_ids([4], 4, "ids", distinct=True)
+    with pytest.raises(ValueError, match="out of range"):
+        ops.host_ids([-1], 4, "ids", distinct=True)
+    with pytest.raises(ValueError, match="duplicate"):
+        ops.host_ids([2, 2], 4, "ids", distinct=True)
+    assert ops.host_ids(np.array([2, 2]), 4, "ids", distinct=False) == [2, 2]
+    assert ops.host_ids(torch.tensor([0, 3]), 4, "ids", distinct=True) == [0, 3]
+
+
+def test_host_cu_validation():
+    assert ops._host_cu([0, 3, 3, 7], 7) == [0, 3, 3, 7]
+    for bad in ([1, 7], [0, 5], [0, 4, 3, 7], []):
+        with pytest.raises(ValueError):
+            ops._host_cu(bad, 7)
+
+
+def test_slot_view_describes_bank_tensors():
+    L, S, H, D = 3, 5, 2, 6
+    wkv = torch.zeros((L, S + 1, H, 64, 64))
+    assert ops.slot_view(wkv, 1) == (L, (S + 1) * H * 4096 * 4, H * 4096 * 4, S + 1, H * 4096 * 4)
+    shift = torch.zeros((L, 2, S + 1, D), dtype=torch.bfloat16)
+    assert ops.slot_view(shift, 2) == (2 * L, (S + 1) * D * 2, D * 2, S + 1, D * 2)
+    assert ops.slot_view(wkv[1], 0) == (1, 0, H * 4096 * 4, S + 1, H * 4096 * 4)
+    with pytest.raises(ValueError):
+        ops.slot_view(wkv.transpose(3, 4), 1)
+    with pytest.raises(ValueError):
+        ops.slot_view(shift.transpose(0, 1), 2)
+
+
+def test_runner_argument_errors():
+    class FakeBank:
+        class layout:
+            n_layer = 2
+        device = torch.device("cpu")
+        num_slots = 4
+
+    with pytest.raises(ValueError):
+        WKV7Runner(FakeBank(), prefill_chunk=0)
+    run = WKV7Runner(FakeBank(), prefill_chunk=64)
+    empty = tuple(torch.zeros((0, 2, 64), dtype=torch.bfloat16) for _ in range(6))
+    with pytest.raises(ValueError, match="empty prompt"):
+        run.prefill([empty, empty], {"wkv": 1, "shift": 1})
+    with pytest.raises(ValueError, match="layers"):
+        run.prefill([empty], {"wkv": 1, "shift": 1})
+    one = _vecs(1, 2)
+    with pytest.raises(ValueError, match="mismatch"):
+        run.decode_step([{"wkv": 1, "shift": 1}, {"wkv": 2, "shift": 2}], [one, one])
+
+
+# -- synthetic inputs ---------------------------------------------------------------------------
+
+def test_synthetic_distributions_and_determinism():
+    g1, g2 = synthetic.make_generator(7), synthetic.make_generator(7)
+    a1 = synthetic.wkv7_vectors((32, 4, 64), g1)
+    a2 = synthetic.wkv7_vectors((32, 4, 64), g2)
+    for n in "rwkvab":
+        assert a1[n].dtype == torch.bfloat16
+        assert torch.equal(a1[n], a2[n])
+    decay = torch.exp(a1["w"].float())
+    assert decay.min() > 0.544 and decay.max() < 1.0
+    kn = -a1["a"].float()
+    assert torch.allclose(kn.norm(dim=-1), torch.ones(32, 4), atol=1e-2)
+    ratio = a1["b"].float() / kn
+    assert ratio.min() > -1e-3 and ratio.max() < 1.0 + 1e-2
+    ids = synthetic.active_slots(16, 4, synthetic.make_generator(3))
+    assert len(set(ids)) == 4 and min(ids) >= 1 and max(ids) <= 16
+    lens = synthetic.ragged_lengths(64, 1, 2048, synthetic.make_generator(4))
+    assert min(lens) >= 1 and max(lens) <= 2048

@@ -1,0 +1,16 @@
+// Library-level entry points of the C ABI: version and error text.
+#include "wkv7_common.h"
+
+extern "C" int wkv7_abi_version(void) { return WKV7_ABI_VERSION; }
+
+extern "C" const char* wkv7_strerror(int code) {
+  switch (code) {
+    case WKV7_OK: return "success";
+    case WKV7_ERR_ARG: return "invalid argument (null pointer, negative size or bad enum)";
+    case WKV7_ERR_SHAPE: return "unsupported shape (head size must be 64; row size within slot stride)";
+    case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_prefill_workspace_bytes()";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown wkv7 error";
+}

@@ -1,0 +1,374 @@
+"""Tensor-level WKV7 ops over the slot pool, bound to libwkv7.so.
+
+Everything here launches the hand-written gfx950 kernels through the C ABI on
+the current torch stream; PyTorch only supplies device memory and the stream.
+There is no CPU or eager fallback: a missing library or a CPU tensor raises.
+
+Two layers of API:
+
+* slot-indexed ops (the hot path): ``wkv7_decode_slots``,
+  ``wkv7_prefill_varlen``, ``slot_copy``, ``slot_zero``;
+* the fla wkv-op signatures the reference's model layer calls
+  (``fused_recurrent_rwkv7`` for T < 64 and ``chunk_rwkv7`` otherwise,
+  dispatched at wkvm/models/rwkv7.py:108-111), implemented by treating the
+  ``[N, H, K, V]`` state tensor as a slot pool with ids ``0..N-1``.
+
+Error behaviour mirrors the reference: invalid arguments raise ``ValueError``
+(wkvm/runner/runner.py:34-35,48-49,78-79 style); a failed launch raises
+``WKV7Error``.
+"""
+
+from __future__ import annotations
+
+from typing import Iterable, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .layout import HEAD_SIZE
+
+_IDS = (list, tuple, range, np.ndarray)
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda(t: torch.Tensor, what: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{what} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor (the WKV7 ops have no CPU path)")
+
+
+def _check_pool(pool: torch.Tensor) -> tuple[int, int]:
+    _require_cuda(pool, "wkv pool")
+    if pool.dtype != torch.float32:
+        raise ValueError(f"wkv pool must be float32, got {pool.dtype}")
+    if pool.dim() != 4 or pool.shape[2] != HEAD_SIZE or pool.shape[3] != HEAD_SIZE:
+        raise ValueError(f"wkv pool must be [rows, H, 64, 64], got {tuple(pool.shape)}")
+    if not pool.is_contiguous():
+        raise ValueError("wkv pool layer must be contiguous")
+    return int(pool.shape[0]), int(pool.shape[1])
+
+
+def host_ids(ids, rows: int, what: str, distinct: bool) -> list[int]:
+    """Validate host-side slot ids: in [0, rows) and (optionally) distinct."""
+    if isinstance(ids, torch.Tensor):
+        ids = ids.tolist()
+    out = [int(i) for i in ids]
+    for i in out:
+        if i < 0 or i >= rows:
+            raise ValueError(f"{what}: slot id {i} out of range [0, {rows})")
+    if distinct and len(set(out)) != len(out):
+        raise ValueError(f"{what}: duplicate slot ids {out}")
+    return out
+
+
+def device_ids(ids, rows: int, device: torch.device, what: str, distinct: bool = True) -> torch.Tensor:
+    """Slot ids as a device int32 tensor.
+
+    Host ids (list / tuple / numpy / CPU tensor) are validated first and raise
+    ``ValueError``. A CUDA int32 tensor is taken as already validated: the
+    kernels skip out-of-range rows without touching memory, and duplicate ids
+    in a write set race.
+    """
+    if isinstance(ids, torch.Tensor) and ids.is_cuda:
+        if ids.dtype != torch.int32 or ids.dim() != 1:
+            raise ValueError(f"{what}: device ids must be a 1-D int32 tensor")
+        if ids.device != device:
+            raise ValueError(f"{what}: ids on {ids.device}, pool on {device}")
+        return ids
+    lst = host_ids(ids, rows, what, distinct)
+    return torch.tensor(lst, dtype=torch.int32, device=device)
+
+
+def _check_vectors(xs: Sequence[torch.Tensor], shape: tuple[int, ...], device: torch.device,
+                   what: str) -> list[torch.Tensor]:
+    out = []
+    for name, x in zip("rwkvab", xs):
+        _require_cuda(x, f"{what}.{name}")
+        if x.dtype != torch.bfloat16:
+            raise ValueError(f"{what}.{name} must be bfloat16, got {x.dtype}")
+        if tuple(x.shape) != shape:
+            raise ValueError(f"{what}.{name} must be {shape}, got {tuple(x.shape)}")
+        if x.device != device:
+            raise ValueError(f"{what}.{name} on {x.device}, pool on {device}")
+        out.append(x.contiguous())
+    return out
+
+
+def _y_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.WKV7_Y_BF16
+    if dtype == torch.float32:
+        return _lib.WKV7_Y_F32
+    raise ValueError(f"y dtype must be bfloat16 or float32, got {dtype}")
+
+
+def _out(out: torch.Tensor | None, shape, dtype, device, what: str) -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _require_cuda(out, what)
+    if tuple(out.shape) != tuple(shape) or not out.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous {tuple(shape)} tensor")
+    return out
+
+
+# -- slot-indexed hot path ---------------------------------------------------------
+
+def wkv7_decode_slots(wkv_layer: torch.Tensor, slot_ids, r, w, k, v, a, b, *,
+                      scale: float = 1.0, out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """One decode token per slot, in place on ``wkv_layer`` ([rows, H, 64, 64]).
+
+    ``r, w, k, v, a, b``: bf16 ``[B, H, 64]`` (``w`` is log-decay). Returns
+    ``y`` ``[B, H, 64]`` in ``out_dtype`` (bf16 or fp32).
+    """
+    rows, H = _check_pool(wkv_layer)
+    dev = wkv_layer.device
+    ids = device_ids(slot_ids, rows, dev, "slot_ids", distinct=True)
+    B = int(ids.shape[0])
+    xs = _check_vectors((r, w, k, v, a, b), (B, H, HEAD_SIZE), dev, "decode")
+    code = _y_code(out.dtype if out is not None else out_dtype)
+    y = _out(out, (B, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
+    if B == 0:
+        return y
+    lib = _lib.load()
+    rc = lib.wkv7_decode_slots(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), B,
+                               *[x.data_ptr() for x in xs], y.data_ptr(), code, float(scale),
+                               _stream_ptr(dev))
+    _lib.check(rc, "wkv7_decode_slots")
+    return y
+
+
+def _host_cu(cu, T: int) -> list[int]:
+    if isinstance(cu, torch.Tensor):
+        cu = cu.tolist()
+    lst = [int(c) for c in cu]
+    if not lst or lst[0] != 0 or lst[-1] != T:
+        raise ValueError(f"cu_seqlens must start at 0 and end at total tokens {T}, got {lst[:3]}..")
+    for i in range(len(lst) - 1):
+        if lst[i + 1] < lst[i]:
+            raise ValueError("cu_seqlens must be non-decreasing")
+    if T >= 2**31:
+        raise ValueError("total tokens must fit int32")
+    return lst
+
+
+def prefill_workspace_bytes(H: int, nseq: int, total_tokens: int) -> int:
+    return int(_lib.load().wkv7_prefill_workspace_bytes(int(H), int(nseq), int(total_tokens)))
+
+
+def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, v, a, b, *,
+                        zero_init: bool = False, scale: float = 1.0,
+                        out: torch.Tensor | None = None,
+                        out_dtype: torch.dtype = torch.bfloat16,
+                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Ragged prefill: sequence ``s`` runs tokens ``cu_seqlens[s]:cu_seqlens[s+1]``
+    of the ``[T, H, 64]`` bf16 inputs from slot ``slot_ids[s]`` (or zero state
+    if ``zero_init``) and leaves its final state in that slot. Returns ``y``
+    ``[T, H, 64]``.
+    """
+    rows, H = _check_pool(wkv_layer)
+    dev = wkv_layer.device
+    ids = device_ids(slot_ids, rows, dev, "slot_ids", distinct=True)
+    nseq = int(ids.shape[0])
+    _require_cuda(r, "prefill.r")
+    T = int(r.shape[0]) if r.dim() == 3 else -1
+    xs = _check_vectors((r, w, k, v, a, b), (T, H, HEAD_SIZE), dev, "prefill")
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.is_cuda:
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.shape != (nseq + 1,):
+            raise ValueError("device cu_seqlens must be int32 [nseq + 1]")
+        cu = cu_seqlens
+    else:
+        lst = _host_cu(cu_seqlens, T)
+        if len(lst) != nseq + 1:
+            raise ValueError(f"cu_seqlens has {len(lst)} entries for {nseq} sequences")
+        cu = torch.tensor(lst, dtype=torch.int32, device=dev)
+    code = _y_code(out.dtype if out is not None else out_dtype)
+    y = _out(out, (T, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
+    if nseq == 0:
+        return y
+    lib = _lib.load()
+    need = int(lib.wkv7_prefill_workspace_bytes(H, nseq, T))
+    if need > 0:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        elif workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace needs {need} bytes")
+    ws_ptr = workspace.data_ptr() if (workspace is not None and need > 0) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
+    rc = lib.wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), cu.data_ptr(), nseq,
+                                 T, *[x.data_ptr() for x in xs], y.data_ptr(), code,
+                                 int(bool(zero_init)), float(scale), ws_ptr, ws_bytes,
+                                 _stream_ptr(dev))
+    _lib.check(rc, "wkv7_prefill_varlen")
+    return y
+
+
+# -- slot row copies -----------------------------------------------------------------
+
+def slot_view(t: torch.Tensor, slot_dim: int) -> tuple[int, int, int, int, int]:
+    """Describe ``t`` as ``outer`` blocks of slot rows along ``slot_dim``.
+
+    Returns ``(outer, outer_stride_B, slot_stride_B, rows, row_bytes)``. The
+    dims after ``slot_dim`` must be contiguous and the dims before it must
+    collapse into a single stride.
+    """
+    if slot_dim < 0:
+        slot_dim += t.dim()
+    if not 0 <= slot_dim < t.dim():
+        raise ValueError("slot_dim out of range")
+    es = t.element_size()
+    row_elems = 1
+    expect = 1
+    for d in range(t.dim() - 1, slot_dim, -1):
+        if t.shape[d] != 1 and t.stride(d) != expect:
+            raise ValueError("dims after the slot dim must be contiguous")
+        expect *= t.shape[d]
+        row_elems *= t.shape[d]
+    rows = int(t.shape[slot_dim])
+    slot_stride = t.stride(slot_dim) * es
+    outer = 1
+    outer_stride = 0
+    for d in range(slot_dim - 1, -1, -1):
+        if t.shape[d] == 1:
+            continue
+        if outer == 1:
+            outer_stride = t.stride(d) * es
+        elif t.stride(d) * es != outer_stride * outer:
+            raise ValueError("dims before the slot dim must collapse to one stride")
+        outer *= int(t.shape[d])
+    return outer, outer_stride, slot_stride, rows, row_elems * es
+
+
+def slot_copy(dst: torch.Tensor, dst_ids, src: torch.Tensor, src_ids, slot_dim: int) -> None:
+    """Bit-exact ``dst[..., dst_ids[p], ...] = src[..., src_ids[p], ...]`` along
+    ``slot_dim`` for every pair p. ``None`` ids mean ``0..n-1`` (dense staging
+    side of a gather or scatter). Within one tensor, destination rows must be
+    distinct and disjoint from the source rows (fork into fresh slots)."""
+    _require_cuda(dst, "dst")
+    _require_cuda(src, "src")
+    if dst.dtype != src.dtype or dst.device != src.device:
+        raise ValueError("dst and src must share dtype and device")
+    d_outer, d_os, d_ss, d_rows, d_rb = slot_view(dst, slot_dim)
+    s_outer, s_os, s_ss, s_rows, s_rb = slot_view(src, slot_dim)
+    if d_outer != s_outer or d_rb != s_rb:
+        raise ValueError("dst and src slot rows differ in shape")
+    dev = dst.device
+    if dst_ids is None and src_ids is None:
+        raise ValueError("at least one of dst_ids / src_ids is required")
+    n = None
+    if dst_ids is not None and not (isinstance(dst_ids, torch.Tensor) and dst_ids.is_cuda):
+        dst_ids = host_ids(dst_ids, d_rows, "dst_ids", distinct=True)
+        n = len(dst_ids)
+    if src_ids is not None and not (isinstance(src_ids, torch.Tensor) and src_ids.is_cuda):
+        src_ids = host_ids(src_ids, s_rows, "src_ids", distinct=False)
+        if n is not None and len(src_ids) != n:
+            raise ValueError("dst_ids and src_ids differ in length")
+        n = len(src_ids)
+    if isinstance(dst_ids, list) and isinstance(src_ids, list) and _overlaps(dst, src):
+        if set(dst_ids) & set(src_ids):
+            raise ValueError("fork destination rows overlap source rows")
+    d_t = device_ids(dst_ids, d_rows, dev, "dst_ids") if dst_ids is not None else None
+    s_t = device_ids(src_ids, s_rows, dev, "src_ids", distinct=False) if src_ids is not None else None
+    if n is None:
+        n = int((d_t if d_t is not None else s_t).shape[0])
+    if d_t is None and n > d_rows:
+        raise ValueError(f"dense dst has {d_rows} rows for {n} copies")
+    if s_t is None and n > s_rows:
+        raise ValueError(f"dense src has {s_rows} rows for {n} copies")
+    if n == 0:
+        return
+    rc = _lib.load().wkv7_slot_copy(dst.data_ptr(), d_os, d_ss, d_rows, _ptr(d_t),
+                                    src.data_ptr(), s_os, s_ss, s_rows, _ptr(s_t),
+                                    d_outer, d_rb, n, _stream_ptr(dev))
+    _lib.check(rc, "wkv7_slot_copy")
+
+
+def _overlaps(x: torch.Tensor, y: torch.Tensor) -> bool:
+    return x.untyped_storage().data_ptr() == y.untyped_storage().data_ptr()
+
+
+def slot_zero(t: torch.Tensor, ids, slot_dim: int) -> None:
+    """Zero slot rows ``ids`` of ``t`` along ``slot_dim`` with a fill kernel."""
+    _require_cuda(t, "tensor")
+    outer, os_, ss, rows, rb = slot_view(t, slot_dim)
+    ids_t = device_ids(ids, rows, t.device, "ids", distinct=False)
+    n = int(ids_t.shape[0])
+    if n == 0:
+        return
+    rc = _lib.load().wkv7_slot_zero(t.data_ptr(), os_, ss, rows, ids_t.data_ptr(), outer, rb, n,
+                                    _stream_ptr(t.device))
+    _lib.check(rc, "wkv7_slot_zero")
+
+
+# -- fla wkv-op signatures --------------------------------------------------------------
+
+def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens, head_first):
+    if head_first:
+        r, w, k, v, a, b = (x.transpose(1, 2) for x in (r, w, k, v, a, b))
+    _require_cuda(r, "r")
+    if r.dim() != 4:
+        raise ValueError("inputs must be [B, T, H, K]")
+    B, T, H, K = r.shape
+    if K != HEAD_SIZE:
+        raise ValueError(f"head size must be {HEAD_SIZE}, got {K}")
+    if r.dtype != torch.bfloat16:
+        raise ValueError("the gfx950 WKV7 kernels take bfloat16 inputs")
+    if cu_seqlens is None:
+        nseq = B
+        cu = [i * T for i in range(B + 1)]
+        flat = [x.reshape(B * T, H, K) for x in (r, w, k, v, a, b)]
+    else:
+        if B != 1:
+            raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
+        cu = cu_seqlens
+        nseq = (len(cu) if not isinstance(cu, torch.Tensor) else int(cu.numel())) - 1
+        flat = [x[0] for x in (r, w, k, v, a, b)]
+    dev = r.device
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (nseq, H, K, K):
+            raise ValueError(f"initial_state must be {(nseq, H, K, K)}")
+        pool = initial_state.to(device=dev, dtype=torch.float32).clone().contiguous()
+    else:
+        pool = torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
+    ids = torch.arange(nseq, dtype=torch.int32, device=dev)
+    y = wkv7_prefill_varlen(pool, ids, cu, *flat, zero_init=initial_state is None, scale=scale,
+                            out_dtype=r.dtype)
+    o = y.reshape(B, T, H, K)
+    if head_first:
+        o = o.transpose(1, 2)
+    return o, (pool if output_final_state else None)
+
+
+def fused_recurrent_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=None,
+                          output_final_state: bool = True, cu_seqlens=None,
+                          head_first: bool = False):
+    """fla-signature recurrent WKV7 (the reference's decode / T < 64 path).
+
+    Tensors ``[B, T, H, 64]`` bf16 (``w`` log-decay); ``initial_state``
+    ``[N, H, 64, 64]`` fp32 with N = B, or the number of packed sequences when
+    ``cu_seqlens`` is given. Returns ``(o, final_state)``.
+    """
+    return _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
+                   head_first)
+
+
+def chunk_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=None,
+                output_final_state: bool = True, cu_seqlens=None, head_first: bool = False):
+    """fla-signature chunked WKV7 (the reference's prefill path, T >= 64).
+    Same arguments and results as ``fused_recurrent_rwkv7``."""
+    return _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
+                   head_first)
+
+
+def ids_list(slot_batch: Iterable[dict], family: str) -> list[int]:
+    """Slot ids of one family from a list of arena slot dicts (wkvm/core/arena.py:55-67)."""
+    return [int(s[family]) for s in slot_batch]

@@ -1,0 +1,116 @@
+"""WKV7Runner: the runner's prefill / decode control flow at the WKV-op level.
+
+Mirrors RWKV7Runner (wkvm/runner/runner.py:23-89) with the model forward
+reduced to its WKV7 op: callers hand in the per-layer projected vectors
+(r, w, k, v, a, b) that the RWKV-7 time-mix produces, instead of token ids.
+The control flow is the reference's:
+
+* ``prefill`` walks the prompt in ``prefill_chunk`` slices and, inside each
+  slice, every layer; the state round-trips through the slot between slices
+  exactly as a preempted request's would (runner.py:12-14, 52-62);
+* ``decode_step`` advances a batch of slots by one token through every layer
+  (runner.py:65-89);
+* ``mixed_step`` is one scheduler step with decode rows and ragged prefill
+  rows together, one decode launch plus one varlen prefill launch per layer
+  (the split Engine._execute makes, wkvm/engine.py:142-160, laid out with
+  MixedBatchMetadata-style offsets, wkvm/core/mixed_batch.py:213-270).
+
+Errors mirror the reference: ``ValueError`` for ``prefill_chunk < 1``, an
+empty prompt and a batch / input length mismatch.
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from . import ops
+from .state import RWKV7StateBank
+
+LayerInputs = Sequence[torch.Tensor]  # (r, w, k, v, a, b)
+
+
+class WKV7Runner:
+    def __init__(self, bank: RWKV7StateBank, prefill_chunk: int = 512) -> None:
+        if prefill_chunk < 1:
+            raise ValueError("prefill_chunk must be >= 1")
+        self.bank = bank
+        self.prefill_chunk = prefill_chunk
+        self.device = bank.device
+
+    def _check_layers(self, layer_inputs: Sequence[LayerInputs]) -> None:
+        if len(layer_inputs) != self.bank.layout.n_layer:
+            raise ValueError(f"expected inputs for {self.bank.layout.n_layer} layers, "
+                             f"got {len(layer_inputs)}")
+
+    @torch.inference_mode()
+    def prefill(self, layer_inputs: Sequence[LayerInputs], slots: dict[str, int],
+                out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
+        """Run a prompt's ``[T, H, 64]`` vectors through every layer in chunks,
+        leaving the final state in ``slots``; returns per-layer ``y [T, H, 64]``."""
+        self._check_layers(layer_inputs)
+        T = int(layer_inputs[0][0].shape[0])
+        if T == 0:
+            raise ValueError("empty prompt")
+        H = self.bank.layout.num_heads
+        ys = [torch.empty((T, H, 64), dtype=out_dtype, device=self.device)
+              for _ in layer_inputs]
+        ids = ops.device_ids([slots["wkv"]], self.bank.num_slots + 1, self.device, "slots")
+        for start in range(0, T, self.prefill_chunk):
+            n = min(self.prefill_chunk, T - start)
+            for layer, xs in enumerate(layer_inputs):
+                self.bank.prefill_wkv(layer, ids, [0, n], *(x[start:start + n] for x in xs),
+                                      out=ys[layer][start:start + n])
+        return ys
+
+    @torch.inference_mode()
+    def decode_step(self, slot_batch: list[dict[str, int]],
+                    layer_inputs: Sequence[LayerInputs],
+                    out_dtype: torch.dtype = torch.bfloat16) -> list[torch.Tensor]:
+        """Advance every slot in ``slot_batch`` by one token through every
+        layer; ``layer_inputs[l]`` holds ``[B, H, 64]`` vectors. Returns
+        per-layer ``y [B, H, 64]``."""
+        self._check_layers(layer_inputs)
+        if any(int(x.shape[0]) != len(slot_batch) for xs in layer_inputs for x in xs):
+            raise ValueError("slot_batch and last_tokens length mismatch")
+        ids = ops.device_ids(ops.ids_list(slot_batch, "wkv"), self.bank.num_slots + 1,
+                             self.device, "slot_batch")
+        return [self.bank.decode_wkv(layer, ids, *xs, out_dtype=out_dtype)
+                for layer, xs in enumerate(layer_inputs)]
+
+    @torch.inference_mode()
+    def mixed_step(self, decode_batch: list[dict[str, int]],
+                   decode_inputs: Sequence[LayerInputs],
+                   prefill_batch: list[dict[str, int]], prefill_lens: Sequence[int],
+                   prefill_inputs: Sequence[LayerInputs], *, zero_init: bool = False,
+                   out_dtype: torch.dtype = torch.bfloat16):
+        """One scheduler step over decode rows (one token each) and ragged
+        prefill rows (``prefill_lens`` tokens each, packed along dim 0).
+        Returns ``(decode_ys, prefill_ys)`` per layer."""
+        self._check_layers(decode_inputs)
+        self._check_layers(prefill_inputs)
+        if len(prefill_lens) != len(prefill_batch):
+            raise ValueError("prefill_batch and prefill_lens length mismatch")
+        if any(int(n) < 1 for n in prefill_lens):
+            raise ValueError("prefill rows need at least one token")
+        cu = [0]
+        for n in prefill_lens:
+            cu.append(cu[-1] + int(n))
+        if prefill_batch and any(int(x.shape[0]) != cu[-1] for xs in prefill_inputs for x in xs):
+            raise ValueError("prefill inputs do not hold sum(prefill_lens) tokens")
+        rows = self.bank.num_slots + 1
+        dec_ids = ops.device_ids(ops.ids_list(decode_batch, "wkv"), rows, self.device, "decode")
+        pre_ids = ops.device_ids(ops.ids_list(prefill_batch, "wkv"), rows, self.device, "prefill")
+        if set(ops.ids_list(decode_batch, "wkv")) & set(ops.ids_list(prefill_batch, "wkv")):
+            raise ValueError("a slot cannot decode and prefill in the same step")
+        cu_t = torch.tensor(cu, dtype=torch.int32, device=self.device)
+        dec_ys, pre_ys = [], []
+        for layer in range(self.bank.layout.n_layer):
+            dec_ys.append(self.bank.decode_wkv(layer, dec_ids, *decode_inputs[layer],
+                                               out_dtype=out_dtype)
+                          if decode_batch else None)
+            pre_ys.append(self.bank.prefill_wkv(layer, pre_ids, cu_t, *prefill_inputs[layer],
+                                                zero_init=zero_init, out_dtype=out_dtype)
+                          if prefill_batch else None)
+        return dec_ys, pre_ys
