@@ -57,6 +57,9 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: a few config-1 decode steps plus one "
+                         "1 GiB slot copy (the counter calibration), then exit")
     return ap.parse_args()
 
 
@@ -380,7 +383,7 @@ def cpu_baseline(args):
             O.port_decode_slots_f32(pool[l], ids, *bits[l])
         steps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or steps >= 20:
+        if el > 10.0 or steps >= 400:
             break
     res = {
         "value": B * steps / el,
@@ -392,6 +395,34 @@ def cpu_baseline(args):
     }
     log(f"cpu baseline: {res['value']:.1f} slot-steps/s on {threads} threads ({steps} steps)")
     return res
+
+
+def pmc_probe(torch, dev, args, launcher):
+    """Config-1 decode launches (24 layers x 3 steps after 1 warm-up step) and
+    one wkv7_slot_copy of exactly 1 GiB read + 1 GiB written, so FETCH_SIZE /
+    WRITE_SIZE per decode dispatch can be scaled by the copy's counts."""
+    from wkvm_amd import synthetic
+
+    L, H, S, B = 24, 32, 512, 256
+    gcpu = synthetic.make_generator(args.seed)
+    ids_t = torch.tensor(synthetic.active_slots(S, B, gcpu), dtype=torch.int32, device=dev)
+    gdev = synthetic.make_generator(args.seed + 1, dev)
+    wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
+    wkv.normal_(0.0, 0.1, generator=gdev)
+    xs = [synthetic.order(synthetic.wkv7_vectors((B, H, 64), gdev)) for _ in range(L)]
+    y = torch.empty((B, H, 64), dtype=torch.bfloat16, device=dev)
+    for _ in range(4):
+        for l in range(L):
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), B, ptrs(xs[l]),
+                            y.data_ptr())
+    src = torch.empty((1024, 1 << 20), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    launcher.copy(dst.data_ptr(), 0, 1 << 20, 1024, None, src.data_ptr(), 0, 1 << 20, 1024, None,
+                  1, 1 << 20, 1024)
+    torch.cuda.synchronize()
+    log("pmc probe done: 96 decode dispatches (first 24 warm-up), 1 GiB calibration copy")
 
 
 def pmc_traffic():
@@ -420,6 +451,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     launcher = Launcher(torch, dev)
+    if args.pmc_probe:
+        pmc_probe(torch, dev, args, launcher)
+        return 0
     dec = bench_decode(torch, dev, args, launcher)
     pre = bench_prefill(torch, dev, args, launcher)
     extra = {}

@@ -50,7 +50,7 @@ extern "C" {
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
-#define WKV7_ERR_SHAPE (-2)     /* head size other than 64, misaligned rows */
+#define WKV7_ERR_SHAPE (-2)     /* row size beyond the slot stride, misaligned inputs */
 #define WKV7_ERR_WORKSPACE (-3) /* workspace missing or too small */
 
 #define WKV7_Y_BF16 0 /* y written as bf16 (round to nearest even) */
@@ -99,7 +99,7 @@ int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
  *   slot_ids      [nseq] int32 (device), distinct
  *   cu_seqlens    [nseq + 1] int32 (device), cu_seqlens[0] = 0,
  *                 non-decreasing, cu_seqlens[nseq] = total_tokens
- *   r..b          [total_tokens, H, 64] bf16
+ *   r..b          [total_tokens, H, 64] bf16, 16-byte aligned (else WKV7_ERR_SHAPE)
  *   y             [total_tokens, H, 64], dtype per y_dtype
  *   workspace     device scratch of at least
  *                 wkv7_prefill_workspace_bytes(H, nseq, total_tokens) bytes

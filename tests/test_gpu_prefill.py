@@ -105,8 +105,8 @@ def test_chunk_split_invariance_through_the_slot(dev):
         finals.append(bank.wkv[:, 2].clone())
         outs.append(torch.stack(ys))
     for f, o in zip(finals[1:], outs[1:]):
-        assert U.rel_l2(U.f64(f), U.f64(finals[0])) <= 1e-5
-        assert U.rel_l2(U.f64(o), U.f64(outs[0])) <= 1e-5
+        assert U.rel_l2(U.f64(f), U.f64(finals[0])) <= 1e-4
+        assert U.rel_l2(U.f64(o), U.f64(outs[0])) <= 1e-4
 
 
 def test_fla_signatures(dev):

@@ -137,10 +137,10 @@ def test_fork_rejects_overlap_and_duplicate_destinations(dev):
 def test_copy_odd_row_sizes_pick_narrower_vectors(dev, row_elems, dtype):
     g = torch.Generator(device=dev).manual_seed(row_elems)
     t = torch.randint(0, 100, (3, 9, row_elems), generator=g, device=dev).to(dtype)
-    before = t.cpu().numpy()
+    before = t.cpu().view(torch.uint8).numpy()   # raw bytes: [3, 9, row_bytes]
     ops.slot_copy(t, [0, 8, 4], t, [3, 3, 6], slot_dim=1)
     exp = O.slot_copy_np(before, 1, [3, 3, 6], [0, 8, 4])
-    assert np.array_equal(t.cpu().numpy(), exp)
+    assert np.array_equal(t.cpu().view(torch.uint8).numpy(), exp)
 
 
 def test_copy_between_tensors_gather_and_scatter(dev):

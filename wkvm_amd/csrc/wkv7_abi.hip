@@ -7,7 +7,7 @@ extern "C" const char* wkv7_strerror(int code) {
   switch (code) {
     case WKV7_OK: return "success";
     case WKV7_ERR_ARG: return "invalid argument (null pointer, negative size or bad enum)";
-    case WKV7_ERR_SHAPE: return "unsupported shape (head size must be 64; row size within slot stride)";
+    case WKV7_ERR_SHAPE: return "unsupported layout (row size beyond the slot stride, or inputs not 16-byte aligned)";
     case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_prefill_workspace_bytes()";
     default: break;
   }

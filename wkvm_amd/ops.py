@@ -99,7 +99,10 @@ def _check_vectors(xs: Sequence[torch.Tensor], shape: tuple[int, ...], device: t
             raise ValueError(f"{what}.{name} must be {shape}, got {tuple(x.shape)}")
         if x.device != device:
             raise ValueError(f"{what}.{name} on {x.device}, pool on {device}")
-        out.append(x.contiguous())
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()  # the kernels read 16-byte vectors
+        out.append(x)
     return out
 
 
