@@ -74,8 +74,8 @@ class Launcher:
         self.check = _lib.check
         self.stream = torch.cuda.current_stream(dev).cuda_stream
 
-    def decode(self, pool, rows, H, ids, B, xs, y):
-        rc = self.lib.wkv7_decode_slots(pool, rows, H, ids, B, *xs, y, 0, 1.0, self.stream)
+    def decode(self, pool, rows, H, ids, order, B, xs, y):
+        rc = self.lib.wkv7_decode_slots(pool, rows, H, ids, order, B, *xs, y, 0, 1.0, self.stream)
         if rc:
             self.check(rc, "wkv7_decode_slots")
 
@@ -95,6 +95,12 @@ def ptrs(xs):
     return [x.data_ptr() for x in xs]
 
 
+def sorted_order(torch, ids, dev):
+    """Batch rows sorted by slot id: the decode kernel's visiting order."""
+    order = sorted(range(len(ids)), key=ids.__getitem__)
+    return torch.tensor(order, dtype=torch.int32, device=dev)
+
+
 def bench_decode(torch, dev, args, launcher):
     """Config 1: 1.5B decode, 256 of 512 slots, 24 layers."""
     from wkvm_amd import synthetic
@@ -103,6 +109,7 @@ def bench_decode(torch, dev, args, launcher):
     gcpu = synthetic.make_generator(args.seed)
     ids = synthetic.active_slots(S, B, gcpu)
     ids_t = torch.tensor(ids, dtype=torch.int32, device=dev)
+    order_t = sorted_order(torch, ids, dev)
     gdev = synthetic.make_generator(args.seed + 1, dev)
     wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
     wkv.normal_(0.0, 0.1, generator=gdev)
@@ -115,13 +122,14 @@ def bench_decode(torch, dev, args, launcher):
     pools = [wkv[l].data_ptr() for l in range(L)]
     y_ptrs = [y.data_ptr() for y in ys]
     idp = ids_t.data_ptr()
+    odp = order_t.data_ptr()
 
     def step(i, events=None):
         s = i % NSETS
         for l in range(L):
             if events is not None:
                 events[2 * l].record()
-            launcher.decode(pools[l], S + 1, H, idp, B, vecs[l][s], y_ptrs[l])
+            launcher.decode(pools[l], S + 1, H, idp, odp, B, vecs[l][s], y_ptrs[l])
             if events is not None:
                 events[2 * l + 1].record()
 
@@ -139,8 +147,7 @@ def bench_decode(torch, dev, args, launcher):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
-    # second pass of the same K steps with an event pair around every launch:
-    # the kernel's average launch duration for the roofline figure
+    # second pass of the same K steps with an event pair around every launch
     per = []
     for i in range(args.steps):
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * L)]
@@ -148,7 +155,12 @@ def bench_decode(torch, dev, args, launcher):
         per.append(evs)
     torch.cuda.synchronize()
     durs = [evs[2 * l].elapsed_time(evs[2 * l + 1]) for evs in per for l in range(L)]
-    avg_launch_ms = sum(durs) / len(durs)
+    # Launches in the timed region run back to back on one stream, so the
+    # region's event time over the launch count is the kernel's average launch
+    # duration (it agrees with rocprofv3's per-kernel average); a pair of events
+    # around every launch adds a few microseconds of its own to each.
+    avg_launch_ms = gpu_ms / (args.steps * L)
+    paired_ms = sum(durs) / len(durs)
     bytes_launch = B * slot_layer_bytes(H)
     res = {
         "slot_steps_per_s": B * args.steps / wall,
@@ -156,10 +168,11 @@ def bench_decode(torch, dev, args, launcher):
         "gpu_ms_per_step": gpu_ms / args.steps,
         "hbm_gbps_step": B * args.steps * L * slot_layer_bytes(H) / wall / 1e9,
         "avg_launch_us": 1e3 * avg_launch_ms,
+        "avg_launch_us_event_pairs": 1e3 * paired_ms,
         "launch_gbps": bytes_launch / (avg_launch_ms * 1e-3) / 1e9,
         "bytes_per_launch": bytes_launch,
         "bytes_per_slot_step": L * slot_layer_bytes(H),
-        "launches": len(durs),
+        "launches": args.steps * L,
     }
     log(f"decode cfg1: {res['slot_steps_per_s']:.0f} slot-steps/s, {res['ms_per_step']:.3f} ms/step, "
         f"launch {res['avg_launch_us']:.1f} us = {res['launch_gbps']:.0f} GB/s")
@@ -241,6 +254,7 @@ def bench_fork_decode_7b(torch, dev, args, launcher):
     wkv.normal_(0.0, 0.1, generator=gdev)
     shift = torch.zeros((L, 2, S + 1, D), dtype=torch.bfloat16, device=dev)
     ids_t = torch.tensor(live, dtype=torch.int32, device=dev)
+    order_t = sorted_order(torch, live, dev)
     xs_keep = [synthetic.order(synthetic.wkv7_vectors((B, H, 64), gdev)) for _ in range(L)]
     xs = [ptrs(x) for x in xs_keep]
     ys = [torch.empty((B, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(L)]
@@ -260,7 +274,8 @@ def bench_fork_decode_7b(torch, dev, args, launcher):
 
     def decode():
         for l in range(L):
-            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), B, xs[l], ys[l].data_ptr())
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), order_t.data_ptr(), B, xs[l],
+                            ys[l].data_ptr())
 
     fork(steps)
     decode()
@@ -317,6 +332,7 @@ def bench_mixed(torch, dev, args, launcher):
     wkv.normal_(0.0, 0.1, generator=gdev)
     pre_t = torch.tensor(pre, dtype=torch.int32, device=dev)
     dec_t = torch.tensor(dec, dtype=torch.int32, device=dev)
+    dec_order = sorted_order(torch, dec, dev)
     cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
     dx = [synthetic.order(synthetic.wkv7_vectors((ND, H, 64), gdev)) for _ in range(L)]
     px = [synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev)) for _ in range(2)]
@@ -328,7 +344,8 @@ def bench_mixed(torch, dev, args, launcher):
 
     def step():
         for l in range(L):
-            launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(), ND, ptrs(dx[l]),
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(), dec_order.data_ptr(), ND,
+                            ptrs(dx[l]),
                             dy.data_ptr())
             launcher.prefill(wkv[l].data_ptr(), S + 1, H, pre_t.data_ptr(), cu_t.data_ptr(), NP, T,
                              ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes)
@@ -405,7 +422,9 @@ def pmc_probe(torch, dev, args, launcher):
 
     L, H, S, B = 24, 32, 512, 256
     gcpu = synthetic.make_generator(args.seed)
-    ids_t = torch.tensor(synthetic.active_slots(S, B, gcpu), dtype=torch.int32, device=dev)
+    ids = synthetic.active_slots(S, B, gcpu)
+    ids_t = torch.tensor(ids, dtype=torch.int32, device=dev)
+    order_t = sorted_order(torch, ids, dev)
     gdev = synthetic.make_generator(args.seed + 1, dev)
     wkv = torch.empty((L, S + 1, H, 64, 64), dtype=torch.float32, device=dev)
     wkv.normal_(0.0, 0.1, generator=gdev)
@@ -413,8 +432,8 @@ def pmc_probe(torch, dev, args, launcher):
     y = torch.empty((B, H, 64), dtype=torch.bfloat16, device=dev)
     for _ in range(4):
         for l in range(L):
-            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), B, ptrs(xs[l]),
-                            y.data_ptr())
+            launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), order_t.data_ptr(), B,
+                            ptrs(xs[l]), y.data_ptr())
     src = torch.empty((1024, 1 << 20), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
@@ -491,6 +510,9 @@ def main() -> int:
             "kernel": "decode_slots_kernel",
             "bytes_per_launch": dec["bytes_per_launch"],
             "avg_launch_us": round(dec["avg_launch_us"], 2),
+            "avg_launch_us_event_pairs": round(dec["avg_launch_us_event_pairs"], 2),
+            "traffic_source": "profiles/decode_cfg1_pmc.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                              "copy-calibrated)",
         },
         "decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()},
         "prefill": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in pre.items()},

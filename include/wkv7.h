@@ -74,11 +74,16 @@ const char *wkv7_strerror(int code);
  *
  *   wkv_layer  [num_rows, H, 64, 64] fp32, updated in place at rows slot_ids[b]
  *   slot_ids   [B] int32 (device); must be distinct (duplicates race)
+ *   row_order  [B] int32 (device) or NULL: the order in which batch rows are
+ *              visited, a permutation of 0..B-1. Results do not depend on it;
+ *              rows sorted by slot id keep the HBM stream inside a few
+ *              neighbouring slot regions and raise bandwidth when slots are
+ *              scattered through the pool. Entries outside [0, B) are skipped.
  *   r..b       [B, H, 64] bf16
  *   y          [B, H, 64], dtype per y_dtype (WKV7_Y_BF16 | WKV7_Y_F32)
  */
 int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
-                      const int32_t *slot_ids, int32_t B,
+                      const int32_t *slot_ids, const int32_t *row_order, int32_t B,
                       const uint16_t *r, const uint16_t *w, const uint16_t *k,
                       const uint16_t *v, const uint16_t *a, const uint16_t *b,
                       void *y, int32_t y_dtype, float scale, void *stream);

@@ -170,3 +170,26 @@ def test_runner_decode_step_all_layers(dev):
                     ys[layer])
     idle = [0, 1, 3, 5, 6, 7, 8, 10]
     assert np.array_equal(bank.wkv[:, idle].cpu().numpy(), before[:, idle])
+
+
+def test_row_order_changes_visiting_order_only(dev):
+    """The slot-sorted visiting order (computed for host ids) and any other
+    permutation passed as row_order give bit-identical states and outputs."""
+    H, S = 8, 40
+    gen = synthetic.make_generator(77)
+    base = synthetic.initial_states((S + 1, H, 64, 64), gen).to(dev)
+    ids = synthetic.active_slots(S, 17, gen)
+    vecs = synthetic.order(synthetic.wkv7_vectors((17, H, 64), gen, device=dev))
+    ids_t = torch.tensor(ids, dtype=torch.int32, device=dev)
+    outs = []
+    for order in (None, list(range(17)), list(range(16, -1, -1))):
+        p = base.clone()
+        ro = None if order is None else torch.tensor(order, dtype=torch.int32, device=dev)
+        src = ids if order is None else ids_t
+        y = ops.wkv7_decode_slots(p, src, *vecs, out_dtype=torch.float32, row_order=ro)
+        outs.append((p, y))
+    for p, y in outs[1:]:
+        assert torch.equal(p, outs[0][0]) and torch.equal(y, outs[0][1])
+    with pytest.raises(ValueError):
+        ops.wkv7_decode_slots(base.clone(), ids_t, *vecs,
+                              row_order=torch.arange(16, dtype=torch.int32, device=dev))

@@ -77,11 +77,11 @@ def test_abi_rejects_bad_arguments_before_any_launch():
     dummy = ctypes.c_void_p(16)
     six = [dummy] * 6
     # decode: negative B, bad y dtype, null pool
-    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, -1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, 1, *six, dummy, 7, 1.0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_decode_slots(None, 5, 2, dummy, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_decode_slots(dummy, 5, 0, dummy, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, 0, *six, dummy, 0, 1.0, None) == _lib.WKV7_OK
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, None, -1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, None, 1, *six, dummy, 7, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(None, 5, 2, dummy, None, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 0, dummy, None, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, None, 0, *six, dummy, 0, 1.0, None) == _lib.WKV7_OK
     # prefill: negative sizes, missing cu_seqlens
     assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, dummy, -1, 0, *six, dummy, 0, 0, 1.0,
                                    None, 0, None) == _lib.WKV7_ERR_ARG

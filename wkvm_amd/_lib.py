@@ -34,7 +34,7 @@ SIGNATURES = {
     "wkv7_abi_version": (ctypes.c_int, []),
     "wkv7_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "wkv7_decode_slots": (ctypes.c_int, [
-        _vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _f32, _vp]),
+        _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _f32, _vp]),
     "wkv7_prefill_varlen": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
         _f32, _vp, _sz, _vp]),

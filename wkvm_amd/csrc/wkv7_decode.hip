@@ -1,76 +1,95 @@
 // Slot-indexed WKV7 decode step (one token per slot), in place on the pool.
 //
-// Mapping: one wavefront per (batch row, head). Lane i owns value column
-// h[:, i] of the 64x64 fp32 head state, 64 values held in VGPRs, so both
-// contractions (p_i = sum_j a_j h[j][i] and y_i = sum_j r_j h'[j][i]) are
-// lane-local: no cross-lane reduction. Row j of the state is 256 contiguous
-// bytes, so each of the 64 row loads/stores of a wave is one fully coalesced
-// 256 B access. The per-token vectors (decay, b, k, scaled r, a) are
-// broadcast from LDS; v_i is per lane. Pure HBM streaming: 32 KiB of state
-// traffic per wave against ~320 FMAs per lane.
+// Mapping: one 256-thread workgroup per (batch row, head). Wave q owns key
+// rows j in [16q, 16q+16) of the 64x64 fp32 head state and lane i owns value
+// column i, so each of the 16 row loads/stores of a wave is one full 256 B
+// state row. The two contractions over j are lane-local partial sums, combined
+// across the four waves through LDS:
+//   p_i = sum_j a_j h[j][i]            (before the update)
+//   h'[j][i] = d_j h[j][i] + b_j p_i + k_j v_i
+//   y_i = sum_j (scale r_j) h'[j][i]
+// The per-token vectors (decay d = exp(w), b, k, scale*r, a) are staged in LDS
+// once per workgroup. State traffic is pure streaming (32 KiB per head, read
+// once and written once), issued with non-temporal hints. Workgroups visit the
+// batch rows in the caller's `row_order` (slot-sorted order keeps the HBM
+// access stream inside a few neighbouring slot regions at a time).
 #include "wkv7_common.h"
 
 namespace wkv7 {
 namespace {
 
+constexpr int kDecWaves = 4;
+constexpr int kRowsPerWave = kHead / kDecWaves;  // 16
+
 template <bool kF32Out>
-__global__ __launch_bounds__(kWave) void decode_slots_kernel(
+__global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
-    const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, void* __restrict__ y,
-    float scale) {
-  __shared__ float4 s_dbkr[kHead];       // (decay, b, k, scale*r) per key index j
-  __shared__ float4 s_a[kHead / 4];      // a, four key indices per entry
-  const int lane = threadIdx.x;
-  const int64_t bh = blockIdx.x;         // batch row * H + head
-  const int64_t row = bh / H;
-  const int64_t head = bh - row * H;
+    const int32_t* __restrict__ row_order, int B, const uint16_t* __restrict__ r,
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ a,
+    const uint16_t* __restrict__ b, void* __restrict__ y, float scale) {
+  __shared__ float4 s_dbkr[kHead];            // (decay, b, k, scale*r) per key row j
+  __shared__ float s_a[kHead];
+  __shared__ float s_part[kDecWaves][kHead];  // per-wave partial p, then partial y
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t pos = blockIdx.x / H;
+  const int64_t head = blockIdx.x - pos * H;
+  int64_t row = pos;
+  if (row_order) {
+    row = row_order[pos];
+    if (row < 0 || row >= B) return;  // uniform: the whole block skips
+  }
   const int64_t slot = slot_ids[row];
-  if (slot < 0 || slot >= num_rows) return;  // uniform: the whole block skips
+  if (slot < 0 || slot >= num_rows) return;
 
-  float* hp = wkv + (slot * H + head) * (kHead * kHead) + lane;
-  float h[kHead];
+  float* hp = wkv + (slot * H + head) * (kHead * kHead) + (kRowsPerWave * wave) * kHead + lane;
+  float h[kRowsPerWave];
 #pragma unroll
-  for (int j = 0; j < kHead; ++j) h[j] = hp[j * kHead];
+  for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hp + j * kHead);
 
-  const int64_t io = bh * kHead + lane;
-  s_dbkr[lane] = make_float4(expf(bf16_to_f32(w[io])), bf16_to_f32(b[io]), bf16_to_f32(k[io]),
-                             bf16_to_f32(r[io]) * scale);
-  reinterpret_cast<float*>(s_a)[lane] = bf16_to_f32(a[io]);
+  const int64_t io = (row * H + head) * kHead + lane;
+  if (wave == 0) {
+    s_dbkr[lane] = make_float4(expf(bf16_to_f32(w[io])), bf16_to_f32(b[io]), bf16_to_f32(k[io]),
+                               bf16_to_f32(r[io]) * scale);
+    s_a[lane] = bf16_to_f32(a[io]);
+  }
   const float vi = bf16_to_f32(v[io]);
   __syncthreads();
 
-  // p_i = sum_j a_j h[j][i]; four partial sums keep the FMA chains short.
-  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+  const int j0 = kRowsPerWave * wave;
+  float p0 = 0.f, p1 = 0.f;
 #pragma unroll
-  for (int q = 0; q < kHead / 4; ++q) {
-    const float4 aq = s_a[q];
-    p0 = fmaf(aq.x, h[4 * q + 0], p0);
-    p1 = fmaf(aq.y, h[4 * q + 1], p1);
-    p2 = fmaf(aq.z, h[4 * q + 2], p2);
-    p3 = fmaf(aq.w, h[4 * q + 3], p3);
+  for (int j = 0; j < kRowsPerWave; j += 2) {
+    p0 = fmaf(s_a[j0 + j], h[j], p0);
+    p1 = fmaf(s_a[j0 + j + 1], h[j + 1], p1);
   }
-  const float p = (p0 + p1) + (p2 + p3);
+  s_part[wave][lane] = p0 + p1;
+  __syncthreads();
+  const float p = (s_part[0][lane] + s_part[1][lane]) + (s_part[2][lane] + s_part[3][lane]);
+  __syncthreads();  // partial p read by every wave before it is overwritten
 
-  float y0 = 0.f, y1 = 0.f, y2 = 0.f, y3 = 0.f;
+  float y0 = 0.f, y1 = 0.f;
 #pragma unroll
-  for (int j = 0; j < kHead; ++j) {
-    const float4 c = s_dbkr[j];
+  for (int j = 0; j < kRowsPerWave; ++j) {
+    const float4 c = s_dbkr[j0 + j];
     const float hn = fmaf(c.x, h[j], fmaf(c.y, p, c.z * vi));
-    hp[j * kHead] = hn;
-    switch (j & 3) {
-      case 0: y0 = fmaf(c.w, hn, y0); break;
-      case 1: y1 = fmaf(c.w, hn, y1); break;
-      case 2: y2 = fmaf(c.w, hn, y2); break;
-      default: y3 = fmaf(c.w, hn, y3); break;
-    }
+    __builtin_nontemporal_store(hn, hp + j * kHead);
+    if (j & 1)
+      y1 = fmaf(c.w, hn, y1);
+    else
+      y0 = fmaf(c.w, hn, y0);
   }
-  const float yi = (y0 + y1) + (y2 + y3);
-  if (kF32Out)
-    static_cast<float*>(y)[io] = yi;
-  else
-    static_cast<uint16_t*>(y)[io] = f32_to_bf16(yi);
+  s_part[wave][lane] = y0 + y1;
+  __syncthreads();
+  if (wave == 0) {
+    const float yi = (s_part[0][lane] + s_part[1][lane]) + (s_part[2][lane] + s_part[3][lane]);
+    if (kF32Out)
+      static_cast<float*>(y)[io] = yi;
+    else
+      static_cast<uint16_t*>(y)[io] = f32_to_bf16(yi);
+  }
 }
 
 }  // namespace
@@ -79,10 +98,10 @@ __global__ __launch_bounds__(kWave) void decode_slots_kernel(
 using namespace wkv7;
 
 extern "C" int wkv7_decode_slots(float* wkv_layer, int64_t num_rows, int32_t H,
-                                 const int32_t* slot_ids, int32_t B, const uint16_t* r,
-                                 const uint16_t* w, const uint16_t* k, const uint16_t* v,
-                                 const uint16_t* a, const uint16_t* b, void* y, int32_t y_dtype,
-                                 float scale, void* stream) {
+                                 const int32_t* slot_ids, const int32_t* row_order, int32_t B,
+                                 const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                                 const uint16_t* v, const uint16_t* a, const uint16_t* b, void* y,
+                                 int32_t y_dtype, float scale, void* stream) {
   if (B < 0 || H < 1 || num_rows < 1) return WKV7_ERR_ARG;
   if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
   if (B == 0) return WKV7_OK;
@@ -90,11 +109,12 @@ extern "C" int wkv7_decode_slots(float* wkv_layer, int64_t num_rows, int32_t H,
   const int64_t blocks = int64_t(B) * H;
   if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
   hipStream_t s = as_stream(stream);
+  const unsigned threads = kWave * kDecWaves;
   if (y_dtype == WKV7_Y_F32)
-    decode_slots_kernel<true><<<unsigned(blocks), kWave, 0, s>>>(wkv_layer, num_rows, H, slot_ids,
-                                                                 r, w, k, v, a, b, y, scale);
+    decode_slots_kernel<true><<<unsigned(blocks), threads, 0, s>>>(
+        wkv_layer, num_rows, H, slot_ids, row_order, B, r, w, k, v, a, b, y, scale);
   else
-    decode_slots_kernel<false><<<unsigned(blocks), kWave, 0, s>>>(wkv_layer, num_rows, H, slot_ids,
-                                                                  r, w, k, v, a, b, y, scale);
+    decode_slots_kernel<false><<<unsigned(blocks), threads, 0, s>>>(
+        wkv_layer, num_rows, H, slot_ids, row_order, B, r, w, k, v, a, b, y, scale);
   return launch_status();
 }

@@ -88,6 +88,21 @@ def device_ids(ids, rows: int, device: torch.device, what: str, distinct: bool =
     return torch.tensor(lst, dtype=torch.int32, device=device)
 
 
+def decode_plan(slot_ids, rows: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Device ``(slot_ids, row_order)`` for a decode batch.
+
+    Host ids are validated (in range, distinct) and uploaded together with the
+    batch rows sorted by slot id -- the visiting order that keeps the kernel's
+    HBM stream local -- in one copy. Device ids pass through with no order.
+    """
+    if isinstance(slot_ids, torch.Tensor) and slot_ids.is_cuda:
+        return device_ids(slot_ids, rows, device, "slot_ids"), None
+    lst = host_ids(slot_ids, rows, "slot_ids", distinct=True)
+    order = sorted(range(len(lst)), key=lst.__getitem__)
+    both = torch.tensor(lst + order, dtype=torch.int32, device=device)
+    return both[:len(lst)], both[len(lst):]
+
+
 def _check_vectors(xs: Sequence[torch.Tensor], shape: tuple[int, ...], device: torch.device,
                    what: str) -> list[torch.Tensor]:
     out = []
@@ -127,15 +142,23 @@ def _out(out: torch.Tensor | None, shape, dtype, device, what: str) -> torch.Ten
 
 def wkv7_decode_slots(wkv_layer: torch.Tensor, slot_ids, r, w, k, v, a, b, *,
                       scale: float = 1.0, out: torch.Tensor | None = None,
-                      out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                      out_dtype: torch.dtype = torch.bfloat16,
+                      row_order: torch.Tensor | None = None) -> torch.Tensor:
     """One decode token per slot, in place on ``wkv_layer`` ([rows, H, 64, 64]).
 
     ``r, w, k, v, a, b``: bf16 ``[B, H, 64]`` (``w`` is log-decay). Returns
-    ``y`` ``[B, H, 64]`` in ``out_dtype`` (bf16 or fp32).
+    ``y`` ``[B, H, 64]`` in ``out_dtype`` (bf16 or fp32). ``row_order`` (device
+    int32, a permutation of the batch rows) only sets the visiting order; for
+    host ids the slot-sorted order is computed here.
     """
     rows, H = _check_pool(wkv_layer)
     dev = wkv_layer.device
-    ids = device_ids(slot_ids, rows, dev, "slot_ids", distinct=True)
+    ids, order = decode_plan(slot_ids, rows, dev)
+    if row_order is not None:
+        if not (isinstance(row_order, torch.Tensor) and row_order.is_cuda
+                and row_order.dtype == torch.int32 and row_order.shape == ids.shape):
+            raise ValueError("row_order must be a device int32 tensor shaped like slot_ids")
+        order = row_order
     B = int(ids.shape[0])
     xs = _check_vectors((r, w, k, v, a, b), (B, H, HEAD_SIZE), dev, "decode")
     code = _y_code(out.dtype if out is not None else out_dtype)
@@ -143,7 +166,7 @@ def wkv7_decode_slots(wkv_layer: torch.Tensor, slot_ids, r, w, k, v, a, b, *,
     if B == 0:
         return y
     lib = _lib.load()
-    rc = lib.wkv7_decode_slots(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), B,
+    rc = lib.wkv7_decode_slots(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), _ptr(order), B,
                                *[x.data_ptr() for x in xs], y.data_ptr(), code, float(scale),
                                _stream_ptr(dev))
     _lib.check(rc, "wkv7_decode_slots")

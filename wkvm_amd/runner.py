@@ -74,9 +74,9 @@ class WKV7Runner:
         self._check_layers(layer_inputs)
         if any(int(x.shape[0]) != len(slot_batch) for xs in layer_inputs for x in xs):
             raise ValueError("slot_batch and last_tokens length mismatch")
-        ids = ops.device_ids(ops.ids_list(slot_batch, "wkv"), self.bank.num_slots + 1,
-                             self.device, "slot_batch")
-        return [self.bank.decode_wkv(layer, ids, *xs, out_dtype=out_dtype)
+        ids, order = ops.decode_plan(ops.ids_list(slot_batch, "wkv"), self.bank.num_slots + 1,
+                                     self.device)
+        return [self.bank.decode_wkv(layer, ids, *xs, out_dtype=out_dtype, row_order=order)
                 for layer, xs in enumerate(layer_inputs)]
 
     @torch.inference_mode()
@@ -100,7 +100,7 @@ class WKV7Runner:
         if prefill_batch and any(int(x.shape[0]) != cu[-1] for xs in prefill_inputs for x in xs):
             raise ValueError("prefill inputs do not hold sum(prefill_lens) tokens")
         rows = self.bank.num_slots + 1
-        dec_ids = ops.device_ids(ops.ids_list(decode_batch, "wkv"), rows, self.device, "decode")
+        dec_ids, dec_order = ops.decode_plan(ops.ids_list(decode_batch, "wkv"), rows, self.device)
         pre_ids = ops.device_ids(ops.ids_list(prefill_batch, "wkv"), rows, self.device, "prefill")
         if set(ops.ids_list(decode_batch, "wkv")) & set(ops.ids_list(prefill_batch, "wkv")):
             raise ValueError("a slot cannot decode and prefill in the same step")
@@ -108,7 +108,7 @@ class WKV7Runner:
         dec_ys, pre_ys = [], []
         for layer in range(self.bank.layout.n_layer):
             dec_ys.append(self.bank.decode_wkv(layer, dec_ids, *decode_inputs[layer],
-                                               out_dtype=out_dtype)
+                                               out_dtype=out_dtype, row_order=dec_order)
                           if decode_batch else None)
             pre_ys.append(self.bank.prefill_wkv(layer, pre_ids, cu_t, *prefill_inputs[layer],
                                                 zero_init=zero_init, out_dtype=out_dtype)

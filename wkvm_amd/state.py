@@ -141,12 +141,14 @@ class RWKV7StateBank:
     # -- in-place WKV7 over slot rows (the hot path) ------------------------------------
 
     def decode_wkv(self, layer: int, slot_batch, r, w, k, v, a, b, *, scale: float = 1.0,
-                   out=None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                   out=None, out_dtype: torch.dtype = torch.bfloat16,
+                   row_order=None) -> torch.Tensor:
         """One decode token per slot for ``layer``; ``slot_batch`` is a list of
-        arena slot dicts or a device int32 id tensor. Returns ``y [B, H, 64]``."""
+        arena slot dicts or a device int32 id tensor (then ``row_order`` may
+        give the visiting order, see ``ops.decode_plan``). Returns ``y [B, H, 64]``."""
         ids = slot_batch if isinstance(slot_batch, torch.Tensor) else ops.ids_list(slot_batch, "wkv")
         return ops.wkv7_decode_slots(self.wkv[layer], ids, r, w, k, v, a, b, scale=scale,
-                                     out=out, out_dtype=out_dtype)
+                                     out=out, out_dtype=out_dtype, row_order=row_order)
 
     def prefill_wkv(self, layer: int, slot_batch, cu_seqlens, r, w, k, v, a, b, *,
                     zero_init: bool = False, scale: float = 1.0, out=None,
