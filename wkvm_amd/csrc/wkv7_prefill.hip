@@ -121,10 +121,11 @@ __device__ __forceinline__ f32x4 mma16x2(const uint2& ah, const uint2& al, const
   return mma16(ah, b, c);
 }
 
-// Orders this wave's LDS writes before its later LDS reads by other lanes.
+// Orders this wave's LDS writes before its later LDS reads by other lanes of
+// the same wave. The LDS executes one wave's instructions in order, so only
+// the compiler has to be kept from reordering across this point.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
@@ -175,7 +176,14 @@ __device__ __forceinline__ uint16_t elem_bits(const uint4 (&x)[2], int e) {
   return static_cast<uint16_t>((e & 1) ? (w >> 16) : w);
 }
 
+// Value of the lane one to the left in the DPP row; the first lane gets `first`.
+__device__ __forceinline__ float row_prev(float x, float first) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(x), 0x111, 0xf, 0xf, false));
+}
+
 // Inclusive prefix sum over the 16 lanes of a DPP row (row_shr 1, 2, 4, 8).
+
 template <int kShift>
 __device__ __forceinline__ float row_shr(float x) {
   // lanes whose source falls outside the row receive 0 (the `old` operand)
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
           const float G = row_prefix_sum(w2);  // through token t
           in_[q] = __builtin_amdgcn_exp2f(-G);
           eh[q] = __builtin_amdgcn_exp2f(G);
-          ex[q] = __builtin_amdgcn_exp2f(G - w2);  // through token t-1
+          ex[q] = row_prev(eh[q], 1.f);  // decay through token t-1
           gam_hi[e + q] = eh[q];
         }
         split2(elem(pf.a, e) * ex[0], elem(pf.a, e + 1) * ex[1], ah[e / 2], al[e / 2]);
@@ -317,21 +325,25 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       // T = (I - L_ab)^{-1}, column c = lane, by forward substitution in fp32
       if (lane < kSub) {
         const int c = lane;
+        // all of L (strictly lower, broadcast reads) into registers first
+        float Lr[kSub][kSub];
+#pragma unroll
+        for (int tq = 1; tq < kSub; ++tq)
+#pragma unroll
+          for (int q = 0; q < kSub; q += 4) {
+            if (q >= tq) break;
+            const float4 v4 = *reinterpret_cast<const float4*>(&P1.L[tq * kSub + q]);
+            Lr[tq][q] = v4.x;
+            Lr[tq][q + 1] = v4.y;
+            Lr[tq][q + 2] = v4.z;
+            Lr[tq][q + 3] = v4.w;
+          }
         float tc[kSub];
 #pragma unroll
         for (int tq = 0; tq < kSub; ++tq) {
-          float Lrow[kSub];
-#pragma unroll
-          for (int q = 0; q < kSub; q += 4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(&P1.L[tq * kSub + q]);
-            Lrow[q] = v4.x;
-            Lrow[q + 1] = v4.y;
-            Lrow[q + 2] = v4.z;
-            Lrow[q + 3] = v4.w;
-          }
           float acc = (tq == c) ? 1.f : 0.f;
 #pragma unroll
-          for (int q = 0; q < tq; ++q) acc = fmaf(Lrow[q], tc[q], acc);
+          for (int q = 0; q < tq; ++q) acc = fmaf(Lr[tq][q], tc[q], acc);
           tc[tq] = acc;
         }
 #pragma unroll
@@ -357,6 +369,33 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 #pragma unroll 1
       for (int u = 0; u < kNumSub; ++u) {
         const SubShared& S = sh[u];
+        // shared operands of this sub-chunk, all requested up front
+        uint4 ah[2], al[2], rh[2], rl[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int off = li * kPR + 32 * kb + 8 * lg;
+          ah[kb] = ld16(&S.A[0][off]);
+          al[kb] = ld16(&S.A[1][off]);
+          rh[kb] = ld16(&S.R[0][off]);
+          rl[kb] = ld16(&S.R[1][off]);
+        }
+        const int so = li * kPS + 4 * lg;  // A operand [t = li][s = 4lg..]
+        const uint2 vb = ld8(&S.VT[(col0 + li) * kPS + 4 * lg]);
+        const uint2 lakh = ld8(&S.Lak[0][so]), lakl = ld8(&S.Lak[1][so]);
+        const uint2 th = ld8(&S.T[0][so]), tl = ld8(&S.T[1][so]);
+        const uint2 mrbh = ld8(&S.Mrb[0][so]), mrbl = ld8(&S.Mrb[1][so]);
+        const uint2 mrkh = ld8(&S.Mrk[0][so]), mrkl = ld8(&S.Mrk[1][so]);
+        uint2 bth[4], btl[4], kth[4], ktl[4];
+        float4 gm[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const int jo = (16 * jb + li) * kPS + 4 * lg;  // A operand [j = 16jb + li][s = 4lg..]
+          bth[jb] = ld8(&S.BT[0][jo]);
+          btl[jb] = ld8(&S.BT[1][jo]);
+          kth[jb] = ld8(&S.KT[0][jo]);
+          ktl[jb] = ld8(&S.KT[1][jo]);
+          gm[jb] = *reinterpret_cast<const float4*>(&S.gam[16 * jb + 4 * lg]);
+        }
         // stage the state columns as the B operand [i][j] (hi/lo)
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
@@ -372,23 +411,19 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           const int off = li * kPR + 32 * kb + 8 * lg;
-          const uint4 ah = ld16(&S.A[0][off]), al = ld16(&S.A[1][off]);
-          const uint4 rh = ld16(&S.R[0][off]), rl = ld16(&S.R[1][off]);
           const uint4 hh = ld16(&P2.hT[0][off]), hl = ld16(&P2.hT[1][off]);
-          X = mma32x3(ah, al, hh, hl, X);
-          Z = mma32x3(rh, rl, hh, hl, Z);
+          X = mma32x3(ah[kb], al[kb], hh, hl, X);
+          Z = mma32x3(rh[kb], rl[kb], hh, hl, Z);
         }
-        const int so = li * kPS + 4 * lg;  // A operand [t = li][s = 4lg..]
-        const uint2 vb = ld8(&S.VT[(col0 + li) * kPS + 4 * lg]);
-        X = mma16x2(ld8(&S.Lak[0][so]), ld8(&S.Lak[1][so]), vb, X);  // rhs = A^ h + L_ak V
+        X = mma16x2(lakh, lakl, vb, X);  // rhs = A^ h + L_ak V
         uint2 xh, xl;
         pack_split(X, xh, xl);
         f32x4 Pm = {0.f, 0.f, 0.f, 0.f};
-        Pm = mma16x3(ld8(&S.T[0][so]), ld8(&S.T[1][so]), xh, xl, Pm);  // P = T rhs
+        Pm = mma16x3(th, tl, xh, xl, Pm);  // P = T rhs
         uint2 ph, pl;
         pack_split(Pm, ph, pl);
-        Z = mma16x3(ld8(&S.Mrb[0][so]), ld8(&S.Mrb[1][so]), ph, pl, Z);
-        Z = mma16x2(ld8(&S.Mrk[0][so]), ld8(&S.Mrk[1][so]), vb, Z);
+        Z = mma16x3(mrbh, mrbl, ph, pl, Z);
+        Z = mma16x2(mrkh, mrkl, vb, Z);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int64_t tok = c0 + kSub * u + 4 * lg + rr;
@@ -402,11 +437,12 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
         }
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-          const int jo = (16 * jb + li) * kPS + 4 * lg;  // A operand [j = 16jb + li][s = 4lg..]
-          h[jb] = mma16x3(ld8(&S.BT[0][jo]), ld8(&S.BT[1][jo]), ph, pl, h[jb]);
-          h[jb] = mma16x2(ld8(&S.KT[0][jo]), ld8(&S.KT[1][jo]), vb, h[jb]);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) h[jb][rr] *= S.gam[16 * jb + 4 * lg + rr];
+          h[jb] = mma16x3(bth[jb], btl[jb], ph, pl, h[jb]);
+          h[jb] = mma16x2(kth[jb], ktl[jb], vb, h[jb]);
+          h[jb][0] *= gm[jb].x;
+          h[jb][1] *= gm[jb].y;
+          h[jb][2] *= gm[jb].z;
+          h[jb][3] *= gm[jb].w;
         }
         wave_sync();
       }
