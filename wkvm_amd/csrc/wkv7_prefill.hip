@@ -1,11 +1,11 @@
 // Varlen WKV7 prefill over slot states: chunked scan on MFMA.
 //
-// One workgroup (4 wavefronts) walks one (sequence, head) in 64-token chunks;
-// the 64x64 fp32 state stays in MFMA accumulator registers for the whole
-// sequence (wave q owns value columns [16q, 16q+16)) and touches HBM only to
-// load the slot state at the start and store it at the end.
+// One workgroup (8 wavefronts) walks one (sequence, head). The 64x64 fp32
+// state stays in MFMA accumulator registers for the whole sequence (state
+// wave q owns value columns [16q, 16q+16)) and touches HBM only to load the
+// slot state at the start and store it at the end.
 //
-// A chunk is solved as four 16-token sub-chunks. With G_t the inclusive
+// The sequence is solved in 16-token sub-chunks. With G_t the inclusive
 // cumulative log-decay inside a sub-chunk (G_{-1} = 0):
 //   A^_t = a_t e^{G_{t-1}}   R^_t = scale r_t e^{G_t}   B~_s = b_s e^{-G_s}   K~_s = k_s e^{-G_s}
 //   L_ab = tril(A^ B~^T, -1)  L_ak = tril(A^ K~^T, -1)  M_rb = tril(R^ B~^T)  M_rk = tril(R^ K~^T)
@@ -13,23 +13,34 @@
 //   Y  = R^ h + M_rb P + M_rk V
 //   h' = diag(e^{G_15}) (h + B~^T P + K~^T V)
 // Sub-chunk referencing keeps every decay factor within e^{+-16 |w|}, far from
-// fp32/bf16 range limits. Padding tokens past the end of a sequence enter as
-// w = 0 (decay 1) and zero vectors, i.e. identity steps.
+// fp32/bf16 range limits for RWKV-7's decays (|w| < 0.61 per token). Padding
+// tokens past the end of a sequence enter as w = 0 (decay 1) and zero
+// vectors, i.e. identity steps.
 //
-// Phase I (state independent, wave u builds sub-chunk u): decays, the four
-// operand matrices, the four 16x16 scores and T = (I - L_ab)^{-1} (forward
-// substitution in fp32), all staged in LDS. Phase II (state chain, wave q for
-// its 16 columns, sub-chunks in order): the products above on MFMA.
+// Schedule: a four-deep software pipeline over sub-chunks, one workgroup
+// barrier per tick. In tick k the four state waves run sub-chunk k's state
+// step (the products above for their value columns) while the four operand
+// waves prepare the sub-chunks ahead:
+//   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
+//   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave
+//   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
+//                              per wave
+// Sub-chunk j lives in ring slot j % 4 from tick j-3 to tick j; its inputs
+// are loaded two ticks before they are used.
 //
 // Precision: every MFMA operand that is not an exact bf16 input is split into
 // bf16 hi + lo parts and a product is formed as hi*hi + hi*lo + lo*hi with
 // fp32 accumulation (~2^-16 relative per product); products with the exact
-// bf16 v need two MFMAs. Operand layouts used below (v_mfma_f32_16x16x32_bf16,
-// lane l, li = l%16, lg = l/16): A lane holds A[li][8lg..8lg+7] of a 32-wide k
-// block, B lane holds B[8lg..8lg+7][li], the accumulator holds D[4lg..4lg+3][li].
-// Contractions over 16 tokens put k = 4lg..4lg+3 in elements 0..3 of both
-// operands and zeros in 4..7; with that labelling a 16x16 accumulator is
-// already the B operand of the next 16-token product, straight from registers.
+// bf16 v need two MFMAs. T is solved in fp32. Operand layouts below
+// (v_mfma_f32_16x16x32_bf16, lane l, li = l%16, lg = l/16): A lane holds
+// A[li][8lg..8lg+7] of a 32-wide k block, B lane holds B[8lg..8lg+7][li], the
+// accumulator holds D[4lg..4lg+3][li]. Contractions over 16 tokens put
+// k = 4lg..4lg+3 in elements 0..3 of both operands and zeros in 4..7; with
+// that labelling a 16x16 accumulator is already the B operand of the next
+// 16-token product, straight from registers. Contractions over the 64 key
+// rows take the k labels of a 32-row block in the order the state tiles hold
+// them (key_pos below), so the state is a B operand straight from registers
+// as well.
 #include "wkv7_common.h"
 
 namespace wkv7 {
@@ -38,40 +49,41 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kChunk = 64;
 constexpr int kSub = 16;
-constexpr int kNumSub = kChunk / kSub;
-constexpr int kThreads = 256;
+constexpr int kRing = 4;
+constexpr int kThreads = 512;
 // LDS row pitches (in bf16 elements), padded so that the 16 rows one MFMA
 // operand load touches fall in distinct banks: 144 B rows for the 64-wide
 // arrays, 40 B rows for the 16-wide ones.
 constexpr int kPR = kHead + 8;  // [row][64] arrays
 constexpr int kPS = kSub + 4;   // [row][16] arrays
 
-struct __align__(16) SubShared {
-  uint16_t A[2][kSub * kPR];      // A^ hi/lo  [t][j]
-  uint16_t R[2][kSub * kPR];      // R^ hi/lo  [t][j]
-  uint16_t BT[2][kHead * kPS];    // B~^T hi/lo [j][s]
-  uint16_t KT[2][kHead * kPS];    // K~^T hi/lo [j][s]
-  uint16_t VT[kHead * kPS];       // v^T (exact bf16) [i][s]
-  uint16_t Lak[2][kSub * kPS];    // [t][s]
-  uint16_t Mrb[2][kSub * kPS];
-  uint16_t Mrk[2][kSub * kPS];
-  uint16_t T[2][kSub * kPS];
-  float gam[kHead];               // e^{G_15} per key index
+// Position of key row j in the [t][.] operand arrays. Key rows of the 32-row
+// block kb, as the state tiles h[2kb], h[2kb+1] hold them in lane group lg,
+// are 32kb + 4lg + {0..3} and 32kb + 16 + 4lg + {0..3}; they take k labels
+// 8lg .. 8lg+7 of that block.
+__device__ __forceinline__ int key_pos(int j) {
+  const int kb = j >> 5, jj = j & 31;
+  return 32 * kb + 8 * ((jj >> 2) & 3) + 4 * (jj >> 4) + (jj & 3);
+}
+
+// One sub-chunk's operands.
+struct __align__(16) Slot {
+  uint16_t A[2][kSub * kPR];    // A^ hi/lo [t][key_pos]
+  uint16_t R[2][kSub * kPR];    // R^ hi/lo [t][key_pos]
+  uint16_t BT[2][kHead * kPS];  // B~^T hi/lo [j][s]
+  uint16_t KT[2][kHead * kPS];  // K~^T hi/lo [j][s]
+  uint16_t VT[kHead * kPS];     // v^T [i][s] (exact bf16)
+  uint2 M[4][2][kWave];         // T, L_ak, M_rb, M_rk hi/lo in A-operand lane order
+  float gam[kSub][kHead];       // e^{G_t}; row 15 is the sub-chunk's decay
 };
 
-struct __align__(16) WaveScratch {
-  union {
-    struct {
-      uint16_t Bs[2][kSub * kPR];    // B~ hi/lo [s][j] (score B operand)
-      uint16_t Ks[2][kSub * kPR];    // K~ hi/lo [s][j]
-      float L[kSub * kSub];          // L_ab fp32 [t][s] (broadcast reads only)
-    } p1;
-    struct {
-      uint16_t hT[2][kSub * kPR];    // this wave's state columns, hi/lo [i][j]
-    } p2;
-  };
+struct __align__(16) Shared {
+  Slot slot[kRing];
+  uint16_t Bs[2][2][kSub * kPR];  // B~ hi/lo [s][key_pos] of two sub-chunks
+  uint16_t Ks[2][2][kSub * kPR];  // K~ hi/lo [s][key_pos]
+  float4 Lf[2][kWave];            // L_ab in fp32, A-operand lane order
+  float4 sink[kWave];             // fp32 copies of the other scores (unused)
 };
 
 // x = hi + lo: hi = bf16(x) and lo = bf16(x - hi) (the difference is exact in
@@ -121,68 +133,11 @@ __device__ __forceinline__ f32x4 mma16x2(const uint2& ah, const uint2& al, const
   return mma16(ah, b, c);
 }
 
-// Orders this wave's LDS writes before its later LDS reads by other lanes of
-// the same wave. The LDS executes one wave's instructions in order, so only
-// the compiler has to be kept from reordering across this point.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-struct Inputs {
-  const uint16_t *r, *w, *k, *v, *a, *b;
-};
-
-// One sub-chunk of inputs as lane (t = lane % 16, g = lane / 16) sees it:
-// channels [16g, 16g + 16) of token t for each vector, as 2 x 8 bf16.
-struct SubLoad {
-  uint4 r[2], w[2], k[2], v[2], a[2], b[2];
-};
-
-__device__ __forceinline__ void load_vec(uint4 (&d)[2], const uint16_t* base, int64_t io, bool valid) {
-  const uint4* p = reinterpret_cast<const uint4*>(base + io);
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-  const uint4 x0 = p[0], x1 = p[1];
-  d[0] = valid ? x0 : z;
-  d[1] = valid ? x1 : z;
-}
-
-// Tokens past the end of the sequence load the last real token's row (always
-// in bounds) and are replaced by zeros, so every lane issues its loads
-// unconditionally; zero vectors with w = 0 are identity steps.
-__device__ __forceinline__ void load_sub(SubLoad& d, const Inputs& in, int64_t tok0, int64_t t_end,
-                                         int64_t tstride, int64_t hoff, int lane) {
-  const int64_t tok = tok0 + (lane & 15);
-  const bool valid = tok < t_end;
-  const int64_t io = (valid ? tok : t_end - 1) * tstride + hoff + 16 * (lane >> 4);
-  load_vec(d.r, in.r, io, valid);
-  load_vec(d.w, in.w, io, valid);
-  load_vec(d.k, in.k, io, valid);
-  load_vec(d.v, in.v, io, valid);
-  load_vec(d.a, in.a, io, valid);
-  load_vec(d.b, in.b, io, valid);
-}
-
-// element e (0..15) of a 16-wide bf16 vector held as 2 x uint4
-__device__ __forceinline__ float elem(const uint4 (&x)[2], int e) {
-  const uint4& q = x[e >> 3];
-  const uint32_t w = (e & 6) == 0 ? q.x : (e & 6) == 2 ? q.y : (e & 6) == 4 ? q.z : q.w;
-  return (e & 1) ? bf16_hi(w) : bf16_lo(w);
-}
-__device__ __forceinline__ uint16_t elem_bits(const uint4 (&x)[2], int e) {
-  const uint4& q = x[e >> 3];
-  const uint32_t w = (e & 6) == 0 ? q.x : (e & 6) == 2 ? q.y : (e & 6) == 4 ? q.z : q.w;
-  return static_cast<uint16_t>((e & 1) ? (w >> 16) : w);
-}
-
 // Value of the lane one to the left in the DPP row; the first lane gets `first`.
 __device__ __forceinline__ float row_prev(float x, float first) {
   return __int_as_float(
       __builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(x), 0x111, 0xf, 0xf, false));
 }
-
-// Inclusive prefix sum over the 16 lanes of a DPP row (row_shr 1, 2, 4, 8).
 
 template <int kShift>
 __device__ __forceinline__ float row_shr(float x) {
@@ -190,6 +145,7 @@ __device__ __forceinline__ float row_shr(float x) {
   return __int_as_float(
       __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + kShift, 0xf, 0xf, false));
 }
+// Inclusive prefix sum over the 16 lanes of a DPP row (row_shr 1, 2, 4, 8).
 __device__ __forceinline__ float row_prefix_sum(float x) {
   x += row_shr<1>(x);
   x += row_shr<2>(x);
@@ -198,263 +154,349 @@ __device__ __forceinline__ float row_prefix_sum(float x) {
   return x;
 }
 
+struct Inputs {
+  const uint16_t *r, *w, *k, *v, *a, *b;
+};
+
+struct SeqGeom {
+  int64_t t_beg, t_end;  // token range of the sequence
+  int64_t tstride;       // elements between consecutive tokens (H * 64)
+  int64_t hoff;          // element offset of this head inside a token row
+};
+
+// One sub-chunk of inputs as lane (t = lane % 16, cg = lane / 16) of part p
+// sees it: key channels 16p + 4cg .. 16p + 4cg + 3 of token t, 4 bf16 each.
+struct SubIn {
+  uint2 r, w, k, v, a, b;
+};
+
+// Tokens past the end of the sequence load the last real token's row (always
+// in bounds), so the loads are unconditional; the operand stage replaces them
+// by zeros at the point of use, which keeps the loads in flight until then.
+__device__ __forceinline__ void load_sub(SubIn& d, const Inputs& in, const SeqGeom& g, int64_t j,
+                                         int lane, int part) {
+  const int64_t tok = g.t_beg + kSub * j + (lane & 15);
+  const int64_t io = (tok < g.t_end ? tok : g.t_end - 1) * g.tstride + g.hoff + 16 * part +
+                     4 * (lane >> 4);
+  d.r = *reinterpret_cast<const uint2*>(in.r + io);
+  d.w = *reinterpret_cast<const uint2*>(in.w + io);
+  d.k = *reinterpret_cast<const uint2*>(in.k + io);
+  d.v = *reinterpret_cast<const uint2*>(in.v + io);
+  d.a = *reinterpret_cast<const uint2*>(in.a + io);
+  d.b = *reinterpret_cast<const uint2*>(in.b + io);
+}
+
+// element m (0..3) of 4 bf16 held as a uint2
+__device__ __forceinline__ float elem4(const uint2& x, int m) {
+  const uint32_t w = (m & 2) ? x.y : x.x;
+  return (m & 1) ? bf16_hi(w) : bf16_lo(w);
+}
+__device__ __forceinline__ uint16_t bits4(const uint2& x, int m) {
+  const uint32_t w = (m & 2) ? x.y : x.x;
+  return static_cast<uint16_t>((m & 1) ? (w >> 16) : w);
+}
+
+// Operands of sub-chunk j for key channels [16 part, 16 part + 16).
+__device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int64_t j,
+                                               const SeqGeom& g, int lane, int part, float scale) {
+  Slot& S = sm.slot[j & (kRing - 1)];
+  const int t = lane & 15, cg = lane >> 4;
+  const bool valid = g.t_beg + kSub * j + t < g.t_end;
+  const uint2 z = make_uint2(0u, 0u);
+  const uint2 rv = valid ? raw.r : z, wv = valid ? raw.w : z, kv = valid ? raw.k : z;
+  const uint2 vv = valid ? raw.v : z, av = valid ? raw.a : z, bv = valid ? raw.b : z;
+  constexpr float kLog2e = 1.4426950408889634f;
+  float A_[4], R_[4], B_[4], K_[4], eh[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float G = row_prefix_sum(elem4(wv, m) * kLog2e);  // log2 decay through token t
+    eh[m] = __builtin_amdgcn_exp2f(G);
+    const float ex = row_prev(eh[m], 1.f);                  // decay through token t-1
+    const float ie = __builtin_amdgcn_exp2f(-G);
+    A_[m] = elem4(av, m) * ex;
+    R_[m] = elem4(rv, m) * scale * eh[m];
+    B_[m] = elem4(bv, m) * ie;
+    K_[m] = elem4(kv, m) * ie;
+  }
+  uint2 ah, al, rh, rl, bh, bl, kh, kl;
+  split2(A_[0], A_[1], ah.x, al.x);
+  split2(A_[2], A_[3], ah.y, al.y);
+  split2(R_[0], R_[1], rh.x, rl.x);
+  split2(R_[2], R_[3], rh.y, rl.y);
+  split2(B_[0], B_[1], bh.x, bl.x);
+  split2(B_[2], B_[3], bh.y, bl.y);
+  split2(K_[0], K_[1], kh.x, kl.x);
+  split2(K_[2], K_[3], kh.y, kl.y);
+
+  const int c0 = 16 * part + 4 * cg;       // key channels c0 .. c0+3 (consecutive key_pos)
+  const int ro = t * kPR + key_pos(c0);
+  *reinterpret_cast<uint2*>(&S.A[0][ro]) = ah;
+  *reinterpret_cast<uint2*>(&S.A[1][ro]) = al;
+  *reinterpret_cast<uint2*>(&S.R[0][ro]) = rh;
+  *reinterpret_cast<uint2*>(&S.R[1][ro]) = rl;
+  *reinterpret_cast<uint2*>(&sm.Bs[j & 1][0][ro]) = bh;
+  *reinterpret_cast<uint2*>(&sm.Bs[j & 1][1][ro]) = bl;
+  *reinterpret_cast<uint2*>(&sm.Ks[j & 1][0][ro]) = kh;
+  *reinterpret_cast<uint2*>(&sm.Ks[j & 1][1][ro]) = kl;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int to = (c0 + m) * kPS + t;
+    S.BT[0][to] = bits4(bh, m);
+    S.BT[1][to] = bits4(bl, m);
+    S.KT[0][to] = bits4(kh, m);
+    S.KT[1][to] = bits4(kl, m);
+    S.VT[to] = bits4(vv, m);
+  }
+  *reinterpret_cast<float4*>(&S.gam[t][c0]) = make_float4(eh[0], eh[1], eh[2], eh[3]);
+}
+
+// Score matrix `part` of sub-chunk j (0: L_ab, 1: L_ak, 2: M_rb, 3: M_rk) as
+// the transposed product Y X^T, whose accumulator is the matrix in A-operand
+// lane order.
+__device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, int part) {
+  Slot& S = sm.slot[j & (kRing - 1)];
+  const int li = lane & 15, lg = lane >> 4;
+  const uint16_t* Y = (part & 1) ? &sm.Ks[j & 1][0][0] : &sm.Bs[j & 1][0][0];
+  const uint16_t* X = (part < 2) ? &S.A[0][0] : &S.R[0][0];
+  constexpr int kLo = kSub * kPR;  // hi -> lo array distance
+  f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int off = li * kPR + 32 * kb + 8 * lg;
+    d = mma32x3(ld16(Y + off), ld16(Y + kLo + off), ld16(X + off), ld16(X + kLo + off), d);
+  }
+  // d[r] = M[t = li][s = 4lg + r]; L_* keep s < t, M_* keep s <= t
+  const int lim = li + (part >> 1);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[r] = (4 * lg + r < lim) ? d[r] : 0.f;
+  float4* fdst = (part == 0) ? sm.Lf[j & 1] : sm.sink;
+  fdst[lane] = make_float4(d[0], d[1], d[2], d[3]);
+  uint2 hi, lo;
+  pack_split(d, hi, lo);
+  S.M[part][0][lane] = hi;  // part 0's copy is overwritten by T one tick later
+  S.M[part][1][lane] = lo;
+}
+
+// One forward-substitution step: every lane of a 16-lane DPP row receives
+// lane Q's value (row_newbcast), i.e. T[Q][c] for the row's column c.
+template <int Q>
+__device__ __forceinline__ void subst_steps(float& acc, const float (&Lr)[kSub]) {
+  const float tqc =
+      __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x150 + Q, 0xf, 0xf, false));
+  acc = fmaf(Lr[Q], tqc, acc);  // L[tq][Q] = 0 for Q >= tq
+  if constexpr (Q + 2 < kSub) subst_steps<Q + 1>(acc, Lr);
+}
+
+// Columns 4 part .. 4 part + 3 of T = (I - L_ab)^{-1} of sub-chunk j by
+// forward substitution in fp32: lane (row tq, column c) accumulates
+// T[tq][c] = [tq == c] + sum_{q < tq} L[tq][q] T[q][c]; the lanes of column
+// c form one DPP row, so T[q][c] is a broadcast of lane q of that row.
+__device__ __forceinline__ void stage_inverse(Shared& sm, int64_t j, int lane, int part) {
+  Slot& S = sm.slot[j & (kRing - 1)];
+  const int tq = lane & 15, cl = lane >> 4;
+  const float4* L = sm.Lf[j & 1];
+  float Lr[kSub];  // row tq of L_ab
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 v4 = L[tq + 16 * g];
+    Lr[4 * g] = v4.x;
+    Lr[4 * g + 1] = v4.y;
+    Lr[4 * g + 2] = v4.z;
+    Lr[4 * g + 3] = v4.w;
+  }
+  float acc = (tq == 4 * part + cl) ? 1.f : 0.f;
+  subst_steps<0>(acc, Lr);
+  uint32_t hi, lo;
+  split2(acc, 0.f, hi, lo);
+  // T[tq][4 part + cl] sits in lane tq + 16 part, element cl of the A operand
+  const int o = 4 * (tq + 16 * part) + cl;
+  reinterpret_cast<uint16_t*>(S.M[0][0])[o] = static_cast<uint16_t>(hi);
+  reinterpret_cast<uint16_t*>(S.M[0][1])[o] = static_cast<uint16_t>(lo);
+}
+
+// State chain of sub-chunk j for value columns [16 wave, 16 wave + 16);
+// returns y of tokens 4lg .. 4lg+3 of the sub-chunk, column 16 wave + li.
+__device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], int64_t j,
+                                             int lane, int wave) {
+  const Slot& S = sm.slot[j & (kRing - 1)];
+  const int li = lane & 15, lg = lane >> 4;
+  const int col0 = kSub * wave;
+  uint4 ah[2], al[2], rh[2], rl[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int off = li * kPR + 32 * kb + 8 * lg;
+    ah[kb] = ld16(&S.A[0][off]);
+    al[kb] = ld16(&S.A[1][off]);
+    rh[kb] = ld16(&S.R[0][off]);
+    rl[kb] = ld16(&S.R[1][off]);
+  }
+  const uint2 vb = ld8(&S.VT[(col0 + li) * kPS + 4 * lg]);
+  const uint2 th = S.M[0][0][lane], tl = S.M[0][1][lane];
+  const uint2 lakh = S.M[1][0][lane], lakl = S.M[1][1][lane];
+  const uint2 mrbh = S.M[2][0][lane], mrbl = S.M[2][1][lane];
+  const uint2 mrkh = S.M[3][0][lane], mrkl = S.M[3][1][lane];
+  uint2 bth[4], btl[4], kth[4], ktl[4];
+  float4 gm[4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    const int jo = (16 * jb + li) * kPS + 4 * lg;  // A operand [j = 16jb + li][s = 4lg..]
+    bth[jb] = ld8(&S.BT[0][jo]);
+    btl[jb] = ld8(&S.BT[1][jo]);
+    kth[jb] = ld8(&S.KT[0][jo]);
+    ktl[jb] = ld8(&S.KT[1][jo]);
+    gm[jb] = *reinterpret_cast<const float4*>(&S.gam[kSub - 1][16 * jb + 4 * lg]);
+  }
+  // the state tiles h[2kb], h[2kb+1] as the B operand of key block kb
+  uint4 hbh[2], hbl[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    uint2 h0h, h0l, h1h, h1l;
+    pack_split(h[2 * kb], h0h, h0l);
+    pack_split(h[2 * kb + 1], h1h, h1l);
+    hbh[kb] = make_uint4(h0h.x, h0h.y, h1h.x, h1h.y);
+    hbl[kb] = make_uint4(h0l.x, h0l.y, h1l.x, h1l.y);
+  }
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 X = mma16x2(lakh, lakl, vb, zero);  // L_ak V
+  f32x4 Z = mma16x2(mrkh, mrkl, vb, zero);  // M_rk V
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    X = mma32x3(ah[kb], al[kb], hbh[kb], hbl[kb], X);  // + A^ h
+    Z = mma32x3(rh[kb], rl[kb], hbh[kb], hbl[kb], Z);  // + R^ h
+  }
+  uint2 xh, xl;
+  pack_split(X, xh, xl);
+  const f32x4 P = mma16x3(th, tl, xh, xl, zero);  // P = T (A^ h + L_ak V)
+  uint2 ph, pl;
+  pack_split(P, ph, pl);
+  Z = mma16x3(mrbh, mrbl, ph, pl, Z);  // + M_rb P
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    h[jb] = mma16x2(kth[jb], ktl[jb], vb, h[jb]);
+    h[jb] = mma16x3(bth[jb], btl[jb], ph, pl, h[jb]);
+    h[jb][0] *= gm[jb].x;
+    h[jb][1] *= gm[jb].y;
+    h[jb][2] *= gm[jb].z;
+    h[jb][3] *= gm[jb].w;
+  }
+  return Z;
+}
+
+template <bool kF32Out>
+__device__ __forceinline__ void store_y(void* y, const f32x4& Z, int64_t j, const SeqGeom& g,
+                                        int lane, int wave) {
+  const int li = lane & 15, lg = lane >> 4;
+  const int64_t tok0 = g.t_beg + kSub * j + 4 * lg;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t tok = tok0 + r;
+    if (tok < g.t_end) {
+      const int64_t yo = tok * g.tstride + g.hoff + kSub * wave + li;
+      if (kF32Out)
+        static_cast<float*>(y)[yo] = Z[r];
+      else
+        static_cast<uint16_t*>(y)[yo] = f32_to_bf16(Z[r]);
+    }
+  }
+}
+
+// One tick of the operand side: inverse of sub-chunk k+1, scores of k+2,
+// operands of k+3 (from `cur`, which is then refilled with k+5).
+__device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Inputs& in,
+                                          const SeqGeom& g, int lane, int part, float scale) {
+  stage_inverse(sm, k + 1, lane, part);
+  stage_scores(sm, k + 2, lane, part);
+  stage_operands(sm, cur, k + 3, g, lane, part, scale);
+  load_sub(cur, in, g, k + 5, lane, part);
+  __syncthreads();
+}
+
+// Eight wavefronts: waves 0-3 run the state chain (wave q owns value columns
+// [16q, 16q+16)), waves 4-7 build the operands of the sub-chunks ahead (part
+// p = wave - 4 handles key channels [16p, 16p+16), T columns [4p, 4p+4) and
+// score matrix p). Each SIMD holds one wave of each kind, so the hardware
+// interleaves the state chain's MFMA latencies with the operand work. Both
+// kinds pass the same sequence of barriers: three fill ticks, then one per
+// sub-chunk.
 template <bool kF32Out>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu_seqlens, Inputs in, void* __restrict__ y,
     int64_t total_tokens, int zero_init, float scale) {
-  __shared__ SubShared sh[kNumSub];
-  __shared__ WaveScratch scratch[4];
+  __shared__ Shared sm;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
   const int64_t seq = blockIdx.x / H;
   const int64_t head = blockIdx.x - seq * H;
   const int64_t slot = slot_ids[seq];
   if (slot < 0 || slot >= num_rows) return;  // uniform: the whole block leaves
-  const int64_t t_end = min(max(int64_t(cu_seqlens[seq + 1]), int64_t(0)), total_tokens);
-  const int64_t t_beg = min(max(int64_t(cu_seqlens[seq]), int64_t(0)), t_end);
-  const int64_t tstride = int64_t(H) * kHead;
-  const int64_t hoff = head * kHead;
-  float* hbase = wkv + (slot * H + head) * (kHead * kHead);
-  const int col0 = kSub * wave;  // this wave's value columns [col0, col0 + 16)
+  SeqGeom g;
+  g.t_end = min(max(int64_t(cu_seqlens[seq + 1]), int64_t(0)), total_tokens);
+  g.t_beg = min(max(int64_t(cu_seqlens[seq]), int64_t(0)), g.t_end);
+  g.tstride = int64_t(H) * kHead;
+  g.hoff = head * kHead;
+  const int64_t n_sub = (g.t_end - g.t_beg + kSub - 1) / kSub;
 
-  // State columns of this wave as four 16x16 accumulator tiles (key blocks jb).
-  f32x4 h[4];
+  if (wave < 4) {
+    // ---- state chain ----
+    const int li = lane & 15, lg = lane >> 4;
+    float* hbase = wkv + (slot * H + head) * (kHead * kHead);
+    const int col0 = kSub * wave;  // this wave's value columns [col0, col0 + 16)
+    // State columns of this wave as four 16x16 accumulator tiles (key blocks jb).
+    f32x4 h[4];
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
+    for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      h[jb][rr] = zero_init ? 0.f : hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li];
-
-  SubLoad pf;
-  if (t_beg < t_end) load_sub(pf, in, t_beg + kSub * wave, t_end, tstride, hoff, lane);
-
-  for (int64_t c0 = t_beg; c0 < t_end; c0 += kChunk) {
-    // ---------------- phase I: wave `wave` builds sub-chunk `wave` ----------------
-    {
-      SubShared& S = sh[wave];
-      auto& P1 = scratch[wave].p1;
-      // lane = (token t, channel group g): log2 cumulative decay by a row scan
-      const int t = lane & 15, g = lane >> 4;
-      constexpr float kLog2e = 1.4426950408889634f;
-      uint32_t ah[8], al[8], rh[8], rl[8], bh[8], bl[8], kh[8], kl[8];
-      float gam_hi[16];
-#pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        float ex[2], in_[2], eh[2];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const float w2 = elem(pf.w, e + q) * kLog2e;
-          const float G = row_prefix_sum(w2);  // through token t
-          in_[q] = __builtin_amdgcn_exp2f(-G);
-          eh[q] = __builtin_amdgcn_exp2f(G);
-          ex[q] = row_prev(eh[q], 1.f);  // decay through token t-1
-          gam_hi[e + q] = eh[q];
-        }
-        split2(elem(pf.a, e) * ex[0], elem(pf.a, e + 1) * ex[1], ah[e / 2], al[e / 2]);
-        split2(elem(pf.r, e) * scale * eh[0], elem(pf.r, e + 1) * scale * eh[1], rh[e / 2], rl[e / 2]);
-        split2(elem(pf.b, e) * in_[0], elem(pf.b, e + 1) * in_[1], bh[e / 2], bl[e / 2]);
-        split2(elem(pf.k, e) * in_[0], elem(pf.k, e + 1) * in_[1], kh[e / 2], kl[e / 2]);
-      }
-      const int ro = t * kPR + 16 * g;  // row t, channels 16g.. (row layouts [t][j])
-      auto st32 = [](uint16_t* dst, const uint32_t (&v)[8]) {
-        reinterpret_cast<uint4*>(dst)[0] = make_uint4(v[0], v[1], v[2], v[3]);
-        reinterpret_cast<uint4*>(dst)[1] = make_uint4(v[4], v[5], v[6], v[7]);
-      };
-      st32(&S.A[0][ro], ah);
-      st32(&S.A[1][ro], al);
-      st32(&S.R[0][ro], rh);
-      st32(&S.R[1][ro], rl);
-      st32(&P1.Bs[0][ro], bh);
-      st32(&P1.Bs[1][ro], bl);
-      st32(&P1.Ks[0][ro], kh);
-      st32(&P1.Ks[1][ro], kl);
-      // transposed layouts [j][s]: 16 lanes of a row write 32 contiguous bytes
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int to = (16 * g + e) * kPS + t;
-        const int sh16 = (e & 1) * 16;
-        S.BT[0][to] = static_cast<uint16_t>(bh[e / 2] >> sh16);
-        S.BT[1][to] = static_cast<uint16_t>(bl[e / 2] >> sh16);
-        S.KT[0][to] = static_cast<uint16_t>(kh[e / 2] >> sh16);
-        S.KT[1][to] = static_cast<uint16_t>(kl[e / 2] >> sh16);
-        S.VT[to] = elem_bits(pf.v, e);
-      }
-      if (t == kSub - 1) {
-#pragma unroll
-        for (int e = 0; e < 16; e += 4)
-          *reinterpret_cast<float4*>(&S.gam[16 * g + e]) =
-              make_float4(gam_hi[e], gam_hi[e + 1], gam_hi[e + 2], gam_hi[e + 3]);
-      }
-      wave_sync();
-
-      // scores: rows t = query token, cols s = key token, contraction over j
-      f32x4 lab = {0.f, 0.f, 0.f, 0.f}, lak = lab, mrb = lab, mrk = lab;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int off = li * kPR + 32 * kb + 8 * lg;
-        const uint4 ah = ld16(&S.A[0][off]), al = ld16(&S.A[1][off]);
-        const uint4 rh = ld16(&S.R[0][off]), rl = ld16(&S.R[1][off]);
-        const uint4 bh = ld16(&P1.Bs[0][off]), bl = ld16(&P1.Bs[1][off]);
-        const uint4 kh = ld16(&P1.Ks[0][off]), kl = ld16(&P1.Ks[1][off]);
-        lab = mma32x3(ah, al, bh, bl, lab);
-        lak = mma32x3(ah, al, kh, kl, lak);
-        mrb = mma32x3(rh, rl, bh, bl, mrb);
-        mrk = mma32x3(rh, rl, kh, kl, mrk);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int tq = 4 * lg + rr, s = li;
-        const int o = tq * kPS + s;
-        P1.L[tq * kSub + s] = s < tq ? lab[rr] : 0.f;
-        uint32_t hi, lo;
-        split2(s < tq ? lak[rr] : 0.f, s <= tq ? mrb[rr] : 0.f, hi, lo);
-        S.Lak[0][o] = static_cast<uint16_t>(hi);
-        S.Lak[1][o] = static_cast<uint16_t>(lo);
-        S.Mrb[0][o] = static_cast<uint16_t>(hi >> 16);
-        S.Mrb[1][o] = static_cast<uint16_t>(lo >> 16);
-        split2(s <= tq ? mrk[rr] : 0.f, 0.f, hi, lo);
-        S.Mrk[0][o] = static_cast<uint16_t>(hi);
-        S.Mrk[1][o] = static_cast<uint16_t>(lo);
-      }
-      wave_sync();
-
-      // T = (I - L_ab)^{-1}, column c = lane, by forward substitution in fp32
-      if (lane < kSub) {
-        const int c = lane;
-        // all of L (strictly lower, broadcast reads) into registers first
-        float Lr[kSub][kSub];
-#pragma unroll
-        for (int tq = 1; tq < kSub; ++tq)
-#pragma unroll
-          for (int q = 0; q < kSub; q += 4) {
-            if (q >= tq) break;
-            const float4 v4 = *reinterpret_cast<const float4*>(&P1.L[tq * kSub + q]);
-            Lr[tq][q] = v4.x;
-            Lr[tq][q + 1] = v4.y;
-            Lr[tq][q + 2] = v4.z;
-            Lr[tq][q + 3] = v4.w;
-          }
-        float tc[kSub];
-#pragma unroll
-        for (int tq = 0; tq < kSub; ++tq) {
-          float acc = (tq == c) ? 1.f : 0.f;
-#pragma unroll
-          for (int q = 0; q < tq; ++q) acc = fmaf(Lr[tq][q], tc[q], acc);
-          tc[tq] = acc;
-        }
-#pragma unroll
-        for (int tq = 0; tq < kSub; tq += 2) {
-          uint32_t hi, lo;
-          split2(tc[tq], tc[tq + 1], hi, lo);
-          S.T[0][tq * kPS + c] = static_cast<uint16_t>(hi);
-          S.T[1][tq * kPS + c] = static_cast<uint16_t>(lo);
-          S.T[0][(tq + 1) * kPS + c] = static_cast<uint16_t>(hi >> 16);
-          S.T[1][(tq + 1) * kPS + c] = static_cast<uint16_t>(lo >> 16);
-        }
+      for (int rr = 0; rr < 4; ++rr)
+        h[jb][rr] = zero_init ? 0.f : hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li];
+    if (n_sub > 0) {
+      __syncthreads();  // fill ticks
+      __syncthreads();
+      __syncthreads();
+      for (int64_t k = 0; k < n_sub; ++k) {
+        const f32x4 yv = stage_state(sm, h, k, lane, wave);
+        store_y<kF32Out>(y, yv, k, g, lane, wave);
+        __syncthreads();
       }
     }
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
+  } else if (n_sub > 0) {
+    // ---- operands ahead of the chain ----
+    const int part = wave - 4;
+    SubIn p0, p1;
+    load_sub(p0, in, g, 0, lane, part);
+    load_sub(p1, in, g, 1, lane, part);
+    // fill ticks -3 .. -1 (stages of sub-chunks past the end, if any, work
+    // on zero tokens and are never consumed)
+    stage_operands(sm, p0, 0, g, lane, part, scale);
+    load_sub(p0, in, g, 2, lane, part);
     __syncthreads();
-
-    // prefetch the next chunk's sub-chunk for this wave while phase II runs
-    if (c0 + kChunk < t_end)
-      load_sub(pf, in, c0 + kChunk + kSub * wave, t_end, tstride, hoff, lane);
-
-    // ---------------- phase II: wave `wave` runs its 16 columns ----------------
-    {
-      auto& P2 = scratch[wave].p2;
-#pragma unroll 1
-      for (int u = 0; u < kNumSub; ++u) {
-        const SubShared& S = sh[u];
-        // shared operands of this sub-chunk, all requested up front
-        uint4 ah[2], al[2], rh[2], rl[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const int off = li * kPR + 32 * kb + 8 * lg;
-          ah[kb] = ld16(&S.A[0][off]);
-          al[kb] = ld16(&S.A[1][off]);
-          rh[kb] = ld16(&S.R[0][off]);
-          rl[kb] = ld16(&S.R[1][off]);
-        }
-        const int so = li * kPS + 4 * lg;  // A operand [t = li][s = 4lg..]
-        const uint2 vb = ld8(&S.VT[(col0 + li) * kPS + 4 * lg]);
-        const uint2 lakh = ld8(&S.Lak[0][so]), lakl = ld8(&S.Lak[1][so]);
-        const uint2 th = ld8(&S.T[0][so]), tl = ld8(&S.T[1][so]);
-        const uint2 mrbh = ld8(&S.Mrb[0][so]), mrbl = ld8(&S.Mrb[1][so]);
-        const uint2 mrkh = ld8(&S.Mrk[0][so]), mrkl = ld8(&S.Mrk[1][so]);
-        uint2 bth[4], btl[4], kth[4], ktl[4];
-        float4 gm[4];
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          const int jo = (16 * jb + li) * kPS + 4 * lg;  // A operand [j = 16jb + li][s = 4lg..]
-          bth[jb] = ld8(&S.BT[0][jo]);
-          btl[jb] = ld8(&S.BT[1][jo]);
-          kth[jb] = ld8(&S.KT[0][jo]);
-          ktl[jb] = ld8(&S.KT[1][jo]);
-          gm[jb] = *reinterpret_cast<const float4*>(&S.gam[16 * jb + 4 * lg]);
-        }
-        // stage the state columns as the B operand [i][j] (hi/lo)
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          uint2 hi, lo;
-          pack_split(h[jb], hi, lo);
-          const int o = li * kPR + 16 * jb + 4 * lg;
-          *reinterpret_cast<uint2*>(&P2.hT[0][o]) = hi;
-          *reinterpret_cast<uint2*>(&P2.hT[1][o]) = lo;
-        }
-        wave_sync();
-
-        f32x4 X = {0.f, 0.f, 0.f, 0.f}, Z = X;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const int off = li * kPR + 32 * kb + 8 * lg;
-          const uint4 hh = ld16(&P2.hT[0][off]), hl = ld16(&P2.hT[1][off]);
-          X = mma32x3(ah[kb], al[kb], hh, hl, X);
-          Z = mma32x3(rh[kb], rl[kb], hh, hl, Z);
-        }
-        X = mma16x2(lakh, lakl, vb, X);  // rhs = A^ h + L_ak V
-        uint2 xh, xl;
-        pack_split(X, xh, xl);
-        f32x4 Pm = {0.f, 0.f, 0.f, 0.f};
-        Pm = mma16x3(th, tl, xh, xl, Pm);  // P = T rhs
-        uint2 ph, pl;
-        pack_split(Pm, ph, pl);
-        Z = mma16x3(mrbh, mrbl, ph, pl, Z);
-        Z = mma16x2(mrkh, mrkl, vb, Z);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int64_t tok = c0 + kSub * u + 4 * lg + rr;
-          if (tok < t_end) {
-            const int64_t yo = tok * tstride + hoff + col0 + li;
-            if (kF32Out)
-              static_cast<float*>(y)[yo] = Z[rr];
-            else
-              static_cast<uint16_t*>(y)[yo] = f32_to_bf16(Z[rr]);
-          }
-        }
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          h[jb] = mma16x3(bth[jb], btl[jb], ph, pl, h[jb]);
-          h[jb] = mma16x2(kth[jb], ktl[jb], vb, h[jb]);
-          h[jb][0] *= gm[jb].x;
-          h[jb][1] *= gm[jb].y;
-          h[jb][2] *= gm[jb].z;
-          h[jb][3] *= gm[jb].w;
-        }
-        wave_sync();
-      }
+    stage_scores(sm, 0, lane, part);
+    stage_operands(sm, p1, 1, g, lane, part, scale);
+    load_sub(p1, in, g, 3, lane, part);
+    __syncthreads();
+    stage_inverse(sm, 0, lane, part);
+    stage_scores(sm, 1, lane, part);
+    stage_operands(sm, p0, 2, g, lane, part, scale);
+    load_sub(p0, in, g, 4, lane, part);
+    __syncthreads();
+    // two ticks per iteration so each input buffer keeps its registers
+    // (sub-chunk k+3 of tick k is in p1 for even k, p0 for odd k). The loop
+    // has a single back edge, after the p0 refill: the compiler's memory-wait
+    // placement then knows that p0's loads are younger than p1's and waits
+    // for p1 alone.
+    int64_t k = 0;
+    for (; k + 1 < n_sub; k += 2) {
+      prep_tick(sm, p1, k, in, g, lane, part, scale);
+      prep_tick(sm, p0, k + 1, in, g, lane, part, scale);
     }
-    __syncthreads();
+    if (k < n_sub) prep_tick(sm, p1, k, in, g, lane, part, scale);
   }
-
-#pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
 }
 
 }  // namespace
