@@ -56,7 +56,8 @@ constexpr int kThreads = 512;
 // operand load touches fall in distinct banks: 144 B rows for the 64-wide
 // arrays, 40 B rows for the 16-wide ones.
 constexpr int kPR = kHead + 8;  // [row][64] arrays
-constexpr int kPS = kSub + 4;   // [row][16] arrays
+constexpr int kPQ = 2 * kSub + 8;  // [row][4 token groups][8] arrays (80 B rows)
+constexpr int kPG = kHead + 4;     // gam rows (floats)
 
 // Position of key row j in the [t][.] operand arrays. Key rows of the 32-row
 // block kb, as the state tiles h[2kb], h[2kb+1] hold them in lane group lg,
@@ -71,11 +72,13 @@ __device__ __forceinline__ int key_pos(int j) {
 struct __align__(16) Slot {
   uint16_t A[2][kSub * kPR];    // A^ hi/lo [t][key_pos]
   uint16_t R[2][kSub * kPR];    // R^ hi/lo [t][key_pos]
-  uint16_t BT[2][kHead * kPS];  // B~^T hi/lo [j][s]
-  uint16_t KT[2][kHead * kPS];  // K~^T hi/lo [j][s]
-  uint16_t VT[kHead * kPS];     // v^T [i][s] (exact bf16)
-  uint2 M[4][2][kWave];         // T, L_ak, M_rb, M_rk hi/lo in A-operand lane order
-  float gam[kSub][kHead];       // e^{G_t}; row 15 is the sub-chunk's decay
+  // [j][s]-ordered 16-token operands: row j, token group q = s / 4 holds
+  // the 8 bf16 {hi(s = 4q..4q+3), lo(s = 4q..4q+3)}, one MFMA operand tuple.
+  uint16_t BT[kHead * kPQ];     // B~^T
+  uint16_t KT[kHead * kPQ];     // K~^T
+  uint16_t VT[kHead * kPQ];     // v^T [i][s], exact bf16, stored twice {v, v}
+  uint4 M[4][kWave];            // T, L_ak, M_rb, M_rk as {hi, lo} in A-operand lane order
+  float gam[kSub][kPG];         // e^{G_t}; row 15 is the sub-chunk's decay
 };
 
 struct __align__(16) Shared {
@@ -240,12 +243,13 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
   *reinterpret_cast<uint2*>(&sm.Ks[j & 1][1][ro]) = kl;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const int to = (c0 + m) * kPS + t;
-    S.BT[0][to] = bits4(bh, m);
-    S.BT[1][to] = bits4(bl, m);
-    S.KT[0][to] = bits4(kh, m);
-    S.KT[1][to] = bits4(kl, m);
+    const int to = (c0 + m) * kPQ + 8 * (t >> 2) + (t & 3);
+    S.BT[to] = bits4(bh, m);
+    S.BT[to + 4] = bits4(bl, m);
+    S.KT[to] = bits4(kh, m);
+    S.KT[to + 4] = bits4(kl, m);
     S.VT[to] = bits4(vv, m);
+    S.VT[to + 4] = bits4(vv, m);
   }
   *reinterpret_cast<float4*>(&S.gam[t][c0]) = make_float4(eh[0], eh[1], eh[2], eh[3]);
 }
@@ -273,8 +277,8 @@ __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, in
   fdst[lane] = make_float4(d[0], d[1], d[2], d[3]);
   uint2 hi, lo;
   pack_split(d, hi, lo);
-  S.M[part][0][lane] = hi;  // part 0's copy is overwritten by T one tick later
-  S.M[part][1][lane] = lo;
+  S.M[part][lane] = make_uint4(hi.x, hi.y, lo.x, lo.y);  // part 0's is overwritten by T
+
 }
 
 // One forward-substitution step: every lane of a 16-lane DPP row receives
@@ -309,13 +313,16 @@ __device__ __forceinline__ void stage_inverse(Shared& sm, int64_t j, int lane, i
   uint32_t hi, lo;
   split2(acc, 0.f, hi, lo);
   // T[tq][4 part + cl] sits in lane tq + 16 part, element cl of the A operand
-  const int o = 4 * (tq + 16 * part) + cl;
-  reinterpret_cast<uint16_t*>(S.M[0][0])[o] = static_cast<uint16_t>(hi);
-  reinterpret_cast<uint16_t*>(S.M[0][1])[o] = static_cast<uint16_t>(lo);
+  uint16_t* Tm = reinterpret_cast<uint16_t*>(&S.M[0][tq + 16 * part]);
+  Tm[cl] = static_cast<uint16_t>(hi);
+  Tm[4 + cl] = static_cast<uint16_t>(lo);
 }
 
 // State chain of sub-chunk j for value columns [16 wave, 16 wave + 16);
 // returns y of tokens 4lg .. 4lg+3 of the sub-chunk, column 16 wave + li.
+// 16-token products use both halves of the 32-wide instruction for two
+// terms of one sum: {mh, ml}.{v, v} = M V for an exact v, and
+// {mh, ml}.{ph, ph} + {mh, ml}.{pl, 0} = mh ph + ml ph + mh pl for a split P.
 __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], int64_t j,
                                              int lane, int wave) {
   const Slot& S = sm.slot[j & (kRing - 1)];
@@ -330,20 +337,15 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
     rh[kb] = ld16(&S.R[0][off]);
     rl[kb] = ld16(&S.R[1][off]);
   }
-  const uint2 vb = ld8(&S.VT[(col0 + li) * kPS + 4 * lg]);
-  const uint2 th = S.M[0][0][lane], tl = S.M[0][1][lane];
-  const uint2 lakh = S.M[1][0][lane], lakl = S.M[1][1][lane];
-  const uint2 mrbh = S.M[2][0][lane], mrbl = S.M[2][1][lane];
-  const uint2 mrkh = S.M[3][0][lane], mrkl = S.M[3][1][lane];
-  uint2 bth[4], btl[4], kth[4], ktl[4];
+  const uint4 vv = ld16(&S.VT[(col0 + li) * kPQ + 8 * lg]);  // {v, v}
+  const uint4 tm = S.M[0][lane], lak = S.M[1][lane], mrb = S.M[2][lane], mrk = S.M[3][lane];
+  uint4 bt[4], kt[4];
   float4 gm[4];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
-    const int jo = (16 * jb + li) * kPS + 4 * lg;  // A operand [j = 16jb + li][s = 4lg..]
-    bth[jb] = ld8(&S.BT[0][jo]);
-    btl[jb] = ld8(&S.BT[1][jo]);
-    kth[jb] = ld8(&S.KT[0][jo]);
-    ktl[jb] = ld8(&S.KT[1][jo]);
+    const int jo = (16 * jb + li) * kPQ + 8 * lg;  // A operand [j = 16jb + li][s = 4lg..]
+    bt[jb] = ld16(&S.BT[jo]);
+    kt[jb] = ld16(&S.KT[jo]);
     gm[jb] = *reinterpret_cast<const float4*>(&S.gam[kSub - 1][16 * jb + 4 * lg]);
   }
   // the state tiles h[2kb], h[2kb+1] as the B operand of key block kb
@@ -357,8 +359,8 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
     hbl[kb] = make_uint4(h0l.x, h0l.y, h1l.x, h1l.y);
   }
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 X = mma16x2(lakh, lakl, vb, zero);  // L_ak V
-  f32x4 Z = mma16x2(mrkh, mrkl, vb, zero);  // M_rk V
+  f32x4 X = mma32(lak, vv, zero);  // L_ak V
+  f32x4 Z = mma32(mrk, vv, zero);  // M_rk V
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     X = mma32x3(ah[kb], al[kb], hbh[kb], hbl[kb], X);  // + A^ h
@@ -366,14 +368,19 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   }
   uint2 xh, xl;
   pack_split(X, xh, xl);
-  const f32x4 P = mma16x3(th, tl, xh, xl, zero);  // P = T (A^ h + L_ak V)
+  f32x4 P = mma32(tm, make_uint4(xh.x, xh.y, 0u, 0u), zero);  // th xh (+ tl 0)
+  P = mma32(tm, make_uint4(xl.x, xl.y, xh.x, xh.y), P);     // + th xl + tl xh
   uint2 ph, pl;
   pack_split(P, ph, pl);
-  Z = mma16x3(mrbh, mrbl, ph, pl, Z);  // + M_rb P
+  const uint4 pp = make_uint4(pl.x, pl.y, ph.x, ph.y);  // {pl, ph}
+  const uint4 p0 = make_uint4(ph.x, ph.y, 0u, 0u);      // {ph, 0}
+  Z = mma32(mrb, p0, Z);  // mh ph
+  Z = mma32(mrb, pp, Z);  // + mh pl + ml ph
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
-    h[jb] = mma16x2(kth[jb], ktl[jb], vb, h[jb]);
-    h[jb] = mma16x3(bth[jb], btl[jb], ph, pl, h[jb]);
+    h[jb] = mma32(kt[jb], vv, h[jb]);
+    h[jb] = mma32(bt[jb], p0, h[jb]);
+    h[jb] = mma32(bt[jb], pp, h[jb]);
     h[jb][0] *= gm[jb].x;
     h[jb][1] *= gm[jb].y;
     h[jb][2] *= gm[jb].z;
