@@ -19,9 +19,9 @@
 //
 // Schedule: a four-deep software pipeline over sub-chunks, one workgroup
 // barrier per tick. In tick k the four state waves run sub-chunk k's state
-// step (the products above for their value columns) while the four operand
-// waves prepare the sub-chunks ahead:
+// step (the products above for their value columns) and
 //   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
+// while the four operand waves prepare the sub-chunks further ahead:
 //   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
 //                              per wave
@@ -407,11 +407,10 @@ __device__ __forceinline__ void store_y(void* y, const f32x4& Z, int64_t j, cons
   }
 }
 
-// One tick of the operand side: inverse of sub-chunk k+1, scores of k+2,
-// operands of k+3 (from `cur`, which is then refilled with k+5).
+// One tick of the operand side: scores of sub-chunk k+2, operands of k+3
+// (from `cur`, which is then refilled with k+5).
 __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Inputs& in,
                                           const SeqGeom& g, int lane, int part, float scale) {
-  stage_inverse(sm, k + 1, lane, part);
   stage_scores(sm, k + 2, lane, part);
   stage_operands(sm, cur, k + 3, g, lane, part, scale);
   load_sub(cur, in, g, k + 5, lane, part);
@@ -419,12 +418,12 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
 }
 
 // Eight wavefronts: waves 0-3 run the state chain (wave q owns value columns
-// [16q, 16q+16)), waves 4-7 build the operands of the sub-chunks ahead (part
-// p = wave - 4 handles key channels [16p, 16p+16), T columns [4p, 4p+4) and
-// score matrix p). Each SIMD holds one wave of each kind, so the hardware
-// interleaves the state chain's MFMA latencies with the operand work. Both
-// kinds pass the same sequence of barriers: three fill ticks, then one per
-// sub-chunk.
+// [16q, 16q+16)) and T columns [4q, 4q+4) of the next sub-chunk; waves 4-7
+// build the operands of the sub-chunks ahead (part p = wave - 4 handles key
+// channels [16p, 16p+16) and score matrix p). Each SIMD holds one wave of
+// each kind, so the hardware interleaves the state chain's MFMA latencies
+// with the operand work. Both kinds pass the same sequence of barriers:
+// three fill ticks, then one per sub-chunk.
 template <bool kF32Out>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
@@ -460,9 +459,11 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     if (n_sub > 0) {
       __syncthreads();  // fill ticks
       __syncthreads();
+      stage_inverse(sm, 0, lane, wave);
       __syncthreads();
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
+        stage_inverse(sm, k + 1, lane, wave);
         store_y<kF32Out>(y, yv, k, g, lane, wave);
         __syncthreads();
       }
@@ -487,7 +488,6 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     stage_operands(sm, p1, 1, g, lane, part, scale);
     load_sub(p1, in, g, 3, lane, part);
     __syncthreads();
-    stage_inverse(sm, 0, lane, part);
     stage_scores(sm, 1, lane, part);
     stage_operands(sm, p0, 2, g, lane, part, scale);
     load_sub(p0, in, g, 4, lane, part);
