@@ -407,6 +407,14 @@ __device__ __forceinline__ void store_y(void* y, const f32x4& Z, int64_t j, cons
   }
 }
 
+// Ends a pipeline tick. The scheduling fence keeps the compiler from moving
+// the next tick's arithmetic above the barrier (which would make it wait for
+// input loads issued only one tick earlier).
+__device__ __forceinline__ void end_tick() {
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // One tick of the operand side: scores of sub-chunk k+2, operands of k+3
 // (from `cur`, which is then refilled with k+5).
 __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Inputs& in,
@@ -414,7 +422,7 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
   stage_scores(sm, k + 2, lane, part);
   stage_operands(sm, cur, k + 3, g, lane, part, scale);
   load_sub(cur, in, g, k + 5, lane, part);
-  __syncthreads();
+  end_tick();
 }
 
 // Eight wavefronts: waves 0-3 run the state chain (wave q owns value columns
@@ -465,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
         stage_inverse(sm, k + 1, lane, wave);
         store_y<kF32Out>(y, yv, k, g, lane, wave);
-        __syncthreads();
+        end_tick();
       }
     }
 #pragma unroll
