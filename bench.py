@@ -415,9 +415,10 @@ def cpu_baseline(args):
 
 
 def pmc_probe(torch, dev, args, launcher):
-    """Config-1 decode launches (24 layers x 3 steps after 1 warm-up step) and
-    one wkv7_slot_copy of exactly 1 GiB read + 1 GiB written, so FETCH_SIZE /
-    WRITE_SIZE per decode dispatch can be scaled by the copy's counts."""
+    """Kernels for rocprofv3 --pmc runs: config-1 decode launches (24 layers x
+    3 steps after 1 warm-up step), config-2 prefill launches (1 warm-up + 2),
+    and one wkv7_slot_copy of exactly 1 GiB read + 1 GiB written, so that
+    FETCH_SIZE / WRITE_SIZE per dispatch can be scaled by the copy's counts."""
     from wkvm_amd import synthetic
 
     L, H, S, B = 24, 32, 512, 256
@@ -434,6 +435,22 @@ def pmc_probe(torch, dev, args, launcher):
         for l in range(L):
             launcher.decode(wkv[l].data_ptr(), S + 1, H, ids_t.data_ptr(), order_t.data_ptr(), B,
                             ptrs(xs[l]), y.data_ptr())
+    torch.cuda.synchronize()
+    del wkv, xs, y
+    # config 2 prefill
+    PS, nseq, T = 16, 8, 4096
+    pids = torch.tensor(synthetic.active_slots(PS, nseq, synthetic.make_generator(args.seed + 2)),
+                        dtype=torch.int32, device=dev)
+    cu_t = torch.arange(nseq + 1, dtype=torch.int32, device=dev) * T
+    pool = torch.zeros((PS + 1, H, 64, 64), dtype=torch.float32, device=dev)
+    pxs = synthetic.order(synthetic.wkv7_vectors((nseq * T, H, 64),
+                                                 synthetic.make_generator(args.seed + 3, dev)))
+    py = torch.empty((nseq * T, H, 64), dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        launcher.prefill(pool.data_ptr(), PS + 1, H, pids.data_ptr(), cu_t.data_ptr(), nseq,
+                         nseq * T, ptrs(pxs), py.data_ptr(), 1)
+    torch.cuda.synchronize()
+    del pool, pxs, py
     src = torch.empty((1024, 1 << 20), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
@@ -441,17 +458,23 @@ def pmc_probe(torch, dev, args, launcher):
     launcher.copy(dst.data_ptr(), 0, 1 << 20, 1024, None, src.data_ptr(), 0, 1 << 20, 1024, None,
                   1, 1 << 20, 1024)
     torch.cuda.synchronize()
-    log("pmc probe done: 96 decode dispatches (first 24 warm-up), 1 GiB calibration copy")
+    log("pmc probe done: 96 decode dispatches (first 24 warm-up), 3 prefill dispatches "
+        "(first warm-up), 1 GiB calibration copy")
+
+
+def profile_value(name: str, key: str):
+    """A figure from a committed rocprofv3 summary under profiles/ (None if absent)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    m = re.search(re.escape(key) + r":\s*([0-9.eE+-]+)", open(path).read())
+    return float(m.group(1)) if m else None
 
 
 def pmc_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 PMC summary,
     if present (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel)."""
-    path = os.path.join(ROOT, "profiles", "decode_cfg1_pmc.txt")
-    if not os.path.exists(path):
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
-    return float(m.group(1)) if m else None
+    return profile_value("decode_cfg1_pmc.txt", "traffic_bytes_per_launch")
 
 
 def main() -> int:
@@ -515,7 +538,17 @@ def main() -> int:
                               "copy-calibrated)",
         },
         "decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()},
-        "prefill": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in pre.items()},
+        "prefill": {
+            **{k: (round(v, 6) if isinstance(v, float) else v) for k, v in pre.items()},
+            "pmc": {
+                "mfma_busy_frac": profile_value("prefill_cfg2_pmc.txt", "mfma_busy_frac"),
+                "mfma_executed_tflops": profile_value("prefill_cfg2_pmc.txt",
+                                                      "mfma_executed_tflops"),
+                "traffic_bytes": profile_value("prefill_cfg2_pmc.txt", "traffic_bytes_per_launch"),
+                "source": "profiles/prefill_cfg2_pmc.txt (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES, "
+                          "SQ_INSTS_VALU_MFMA_MOPS_BF16, FETCH_SIZE/WRITE_SIZE)",
+            },
+        },
         **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
            for k, v in extra.items()},
         "cpu_baseline": cpu,
