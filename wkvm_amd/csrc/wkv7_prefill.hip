@@ -1,6 +1,6 @@
 // Varlen WKV7 prefill over slot states: chunked scan on MFMA.
 //
-// One workgroup (8 wavefronts) walks one (sequence, head). The 64x64 fp32
+// One workgroup (12 wavefronts) walks one (sequence, head). The 64x64 fp32
 // state stays in MFMA accumulator registers for the whole sequence (state
 // wave q owns value columns [16q, 16q+16)) and touches HBM only to load the
 // slot state at the start and store it at the end.
@@ -18,10 +18,10 @@
 // vectors, i.e. identity steps.
 //
 // Schedule: a four-deep software pipeline over sub-chunks, one workgroup
-// barrier per tick. In tick k the four state waves run sub-chunk k's state
-// step (the products above for their value columns) and
+// barrier per tick. In tick k four state waves run sub-chunk k's state step
+// (the products above, 16 value columns each) while eight more waves prepare
+// the sub-chunks ahead:
 //   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
-// while the four operand waves prepare the sub-chunks further ahead:
 //   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
 //                              per wave
@@ -51,7 +51,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSub = 16;
 constexpr int kRing = 4;
-constexpr int kThreads = 512;
+constexpr int kThreads = 768;
 // LDS row pitches (in bf16 elements), padded so that the 16 rows one MFMA
 // operand load touches fall in distinct banks: 144 B rows for the 64-wide
 // arrays, 40 B rows for the 16-wide ones.
@@ -103,37 +103,21 @@ __device__ __forceinline__ void pack_split(const f32x4& x, uint2& hi, uint2& lo)
 }
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ uint2 ld8(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
 
 __device__ __forceinline__ f32x4 mma32(const uint4& a, const uint4& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
-// K = 16 product on the 16x16x32 instruction, upper half of k zero-padded.
-// (Results of the legacy 16x16x16 bf16 instruction read back by VALU came out
-// nondeterministically wrong on gfx950 with this toolchain's wait-state
-// insertion; the padded 16x16x32 form costs the same issue slot and is exact.)
-__device__ __forceinline__ f32x4 mma16(const uint2& a, const uint2& b, f32x4 c) {
-  const uint4 a8 = make_uint4(a.x, a.y, 0u, 0u), b8 = make_uint4(b.x, b.y, 0u, 0u);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a8),
-                                                 __builtin_bit_cast(bf16x8, b8), c, 0, 0, 0);
-}
+// (The legacy 16x16x16 bf16 instruction is not used: its results read back by
+// VALU came out nondeterministically wrong on gfx950 with this toolchain's
+// wait-state insertion. 16-token products run on the 16x16x32 instruction
+// with two terms per issue, see stage_state.)
 // (ah + al)(bh + bl) without the lo*lo term, small terms first.
 __device__ __forceinline__ f32x4 mma32x3(const uint4& ah, const uint4& al, const uint4& bh,
                                          const uint4& bl, f32x4 c) {
   c = mma32(al, bh, c);
   c = mma32(ah, bl, c);
   return mma32(ah, bh, c);
-}
-__device__ __forceinline__ f32x4 mma16x3(const uint2& ah, const uint2& al, const uint2& bh,
-                                         const uint2& bl, f32x4 c) {
-  c = mma16(al, bh, c);
-  c = mma16(ah, bl, c);
-  return mma16(ah, bh, c);
-}
-__device__ __forceinline__ f32x4 mma16x2(const uint2& ah, const uint2& al, const uint2& b, f32x4 c) {
-  c = mma16(al, b, c);
-  return mma16(ah, b, c);
 }
 
 // Value of the lane one to the left in the DPP row; the first lane gets `first`.
@@ -144,9 +128,8 @@ __device__ __forceinline__ float row_prev(float x, float first) {
 
 template <int kShift>
 __device__ __forceinline__ float row_shr(float x) {
-  // lanes whose source falls outside the row receive 0 (the `old` operand)
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + kShift, 0xf, 0xf, false));
+  // lanes whose source falls outside the row receive 0 (bound_ctrl)
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x110 + kShift, 0xf, 0xf, true));
 }
 // Inclusive prefix sum over the 16 lanes of a DPP row (row_shr 1, 2, 4, 8).
 __device__ __forceinline__ float row_prefix_sum(float x) {
@@ -206,8 +189,10 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
   const int t = lane & 15, cg = lane >> 4;
   const bool valid = g.t_beg + kSub * j + t < g.t_end;
   const uint2 z = make_uint2(0u, 0u);
-  const uint2 rv = valid ? raw.r : z, wv = valid ? raw.w : z, kv = valid ? raw.k : z;
-  const uint2 vv = valid ? raw.v : z, av = valid ? raw.a : z, bv = valid ? raw.b : z;
+  // r and v of padding tokens only meet zero rows and columns (their k, b
+  // and a are zero, and their y is not stored), so they need no masking.
+  const uint2 rv = raw.r, wv = valid ? raw.w : z, kv = valid ? raw.k : z;
+  const uint2 vv = raw.v, av = valid ? raw.a : z, bv = valid ? raw.b : z;
   constexpr float kLog2e = 1.4426950408889634f;
   float A_[4], R_[4], B_[4], K_[4], eh[4];
 #pragma unroll
@@ -285,8 +270,7 @@ __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, in
 // lane Q's value (row_newbcast), i.e. T[Q][c] for the row's column c.
 template <int Q>
 __device__ __forceinline__ void subst_steps(float& acc, const float (&Lr)[kSub]) {
-  const float tqc =
-      __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x150 + Q, 0xf, 0xf, false));
+  const float tqc = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0x150 + Q, 0xf, 0xf, true));
   acc = fmaf(Lr[Q], tqc, acc);  // L[tq][Q] = 0 for Q >= tq
   if constexpr (Q + 2 < kSub) subst_steps<Q + 1>(acc, Lr);
 }
@@ -415,23 +399,22 @@ __device__ __forceinline__ void end_tick() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// One tick of the operand side: scores of sub-chunk k+2, operands of k+3
-// (from `cur`, which is then refilled with k+5).
+// One tick of an operand wave: operands of sub-chunk k+3 (from `cur`, which
+// is then refilled with k+5).
 __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Inputs& in,
                                           const SeqGeom& g, int lane, int part, float scale) {
-  stage_scores(sm, k + 2, lane, part);
   stage_operands(sm, cur, k + 3, g, lane, part, scale);
   load_sub(cur, in, g, k + 5, lane, part);
   end_tick();
 }
 
-// Eight wavefronts: waves 0-3 run the state chain (wave q owns value columns
-// [16q, 16q+16)) and T columns [4q, 4q+4) of the next sub-chunk; waves 4-7
-// build the operands of the sub-chunks ahead (part p = wave - 4 handles key
-// channels [16p, 16p+16) and score matrix p). Each SIMD holds one wave of
-// each kind, so the hardware interleaves the state chain's MFMA latencies
-// with the operand work. Both kinds pass the same sequence of barriers:
-// three fill ticks, then one per sub-chunk.
+// Twelve wavefronts in three kinds: waves 0-3 run the state chain (wave q
+// owns value columns [16q, 16q+16)); waves 4-7 build operands (part p =
+// wave - 4 handles key channels [16p, 16p+16)); waves 8-11 compute score
+// matrix p and T columns [4p, 4p+4) (p = wave - 8). Each SIMD holds one wave
+// of each kind, so the hardware interleaves the state chain's MFMA latencies
+// with the operand and inverse work. All kinds pass the same sequence of
+// barriers: three fill ticks, then one per sub-chunk.
 template <bool kF32Out>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
@@ -465,13 +448,11 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       for (int rr = 0; rr < 4; ++rr)
         h[jb][rr] = zero_init ? 0.f : hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li];
     if (n_sub > 0) {
-      __syncthreads();  // fill ticks
-      __syncthreads();
-      stage_inverse(sm, 0, lane, wave);
-      __syncthreads();
+      end_tick();  // fill ticks
+      end_tick();
+      end_tick();
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
-        stage_inverse(sm, k + 1, lane, wave);
         store_y<kF32Out>(y, yv, k, g, lane, wave);
         end_tick();
       }
@@ -481,6 +462,21 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
         hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
+  } else if (wave >= 8) {
+    if (n_sub > 0) {
+      const int part = wave - 8;
+      end_tick();
+      stage_scores(sm, 0, lane, part);
+      end_tick();
+      stage_scores(sm, 1, lane, part);
+      stage_inverse(sm, 0, lane, part);
+      end_tick();
+      for (int64_t k = 0; k < n_sub; ++k) {
+        stage_inverse(sm, k + 1, lane, part);
+        stage_scores(sm, k + 2, lane, part);
+        end_tick();
+      }
+    }
   } else if (n_sub > 0) {
     // ---- operands ahead of the chain ----
     const int part = wave - 4;
@@ -492,11 +488,9 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     stage_operands(sm, p0, 0, g, lane, part, scale);
     load_sub(p0, in, g, 2, lane, part);
     __syncthreads();
-    stage_scores(sm, 0, lane, part);
     stage_operands(sm, p1, 1, g, lane, part, scale);
     load_sub(p1, in, g, 3, lane, part);
     __syncthreads();
-    stage_scores(sm, 1, lane, part);
     stage_operands(sm, p0, 2, g, lane, part, scale);
     load_sub(p0, in, g, 4, lane, part);
     __syncthreads();
