@@ -51,7 +51,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSub = 16;
 constexpr int kRing = 4;
-constexpr int kThreads = 768;
+constexpr int kOpWaves = 4;                      // operand wavefronts
+constexpr int kChan = kHead / (4 * kOpWaves);  // key channels per operand lane
+constexpr int kThreads = kWave * (8 + kOpWaves);  // 4 state + operand + 4 score waves
 // LDS row pitches (in bf16 elements), padded so that the 16 rows one MFMA
 // operand load touches fall in distinct banks: 144 B rows for the 64-wide
 // arrays, 40 B rows for the 16-wide ones.
@@ -150,11 +152,23 @@ struct SeqGeom {
   int64_t hoff;          // element offset of this head inside a token row
 };
 
-// One sub-chunk of inputs as lane (t = lane % 16, cg = lane / 16) of part p
-// sees it: key channels 16p + 4cg .. 16p + 4cg + 3 of token t, 4 bf16 each.
+// One sub-chunk of inputs as lane (t = lane % 16, cg = lane / 16) of operand
+// wave p sees it: kChan consecutive key channels starting at kChan (4p + cg)
+// of token t, kChan bf16 per vector (kChan / 2 packed pairs).
 struct SubIn {
-  uint2 r, w, k, v, a, b;
+  uint32_t r[kChan / 2], w[kChan / 2], k[kChan / 2], v[kChan / 2], a[kChan / 2], b[kChan / 2];
 };
+
+template <int N>
+__device__ __forceinline__ void load_pairs(uint32_t (&d)[N], const uint16_t* p) {
+  if constexpr (N == 2) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    d[0] = x.x;
+    d[1] = x.y;
+  } else {
+    d[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
 
 // Tokens past the end of the sequence load the last real token's row (always
 // in bounds), so the loads are unconditional; the operand stage replaces them
@@ -162,81 +176,98 @@ struct SubIn {
 __device__ __forceinline__ void load_sub(SubIn& d, const Inputs& in, const SeqGeom& g, int64_t j,
                                          int lane, int part) {
   const int64_t tok = g.t_beg + kSub * j + (lane & 15);
-  const int64_t io = (tok < g.t_end ? tok : g.t_end - 1) * g.tstride + g.hoff + 16 * part +
-                     4 * (lane >> 4);
-  d.r = *reinterpret_cast<const uint2*>(in.r + io);
-  d.w = *reinterpret_cast<const uint2*>(in.w + io);
-  d.k = *reinterpret_cast<const uint2*>(in.k + io);
-  d.v = *reinterpret_cast<const uint2*>(in.v + io);
-  d.a = *reinterpret_cast<const uint2*>(in.a + io);
-  d.b = *reinterpret_cast<const uint2*>(in.b + io);
+  const int64_t io = (tok < g.t_end ? tok : g.t_end - 1) * g.tstride + g.hoff +
+                     kChan * (4 * part + (lane >> 4));
+  load_pairs(d.r, in.r + io);
+  load_pairs(d.w, in.w + io);
+  load_pairs(d.k, in.k + io);
+  load_pairs(d.v, in.v + io);
+  load_pairs(d.a, in.a + io);
+  load_pairs(d.b, in.b + io);
 }
 
-// element m (0..3) of 4 bf16 held as a uint2
-__device__ __forceinline__ float elem4(const uint2& x, int m) {
-  const uint32_t w = (m & 2) ? x.y : x.x;
-  return (m & 1) ? bf16_hi(w) : bf16_lo(w);
+// element m of packed bf16 pairs
+template <int N>
+__device__ __forceinline__ float elem(const uint32_t (&x)[N], int m) {
+  return (m & 1) ? bf16_hi(x[m >> 1]) : bf16_lo(x[m >> 1]);
 }
-__device__ __forceinline__ uint16_t bits4(const uint2& x, int m) {
-  const uint32_t w = (m & 2) ? x.y : x.x;
-  return static_cast<uint16_t>((m & 1) ? (w >> 16) : w);
+template <int N>
+__device__ __forceinline__ uint16_t elem_bits(const uint32_t (&x)[N], int m) {
+  return static_cast<uint16_t>((m & 1) ? (x[m >> 1] >> 16) : x[m >> 1]);
 }
 
-// Operands of sub-chunk j for key channels [16 part, 16 part + 16).
+// kChan / 2 packed pairs -> an 8- or 4-byte LDS store
+template <int N>
+__device__ __forceinline__ void st_pairs(uint16_t* p, const uint32_t (&x)[N]) {
+  if constexpr (N == 2)
+    *reinterpret_cast<uint2*>(p) = make_uint2(x[0], x[1]);
+  else
+    *reinterpret_cast<uint32_t*>(p) = x[0];
+}
+
+// Operands of sub-chunk j for key channels [4 kChan part, 4 kChan (part + 1)).
 __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int64_t j,
                                                const SeqGeom& g, int lane, int part, float scale) {
+  constexpr int P = kChan / 2;
   Slot& S = sm.slot[j & (kRing - 1)];
   const int t = lane & 15, cg = lane >> 4;
   const bool valid = g.t_beg + kSub * j + t < g.t_end;
-  const uint2 z = make_uint2(0u, 0u);
   // r and v of padding tokens only meet zero rows and columns (their k, b
   // and a are zero, and their y is not stored), so they need no masking.
-  const uint2 rv = raw.r, wv = valid ? raw.w : z, kv = valid ? raw.k : z;
-  const uint2 vv = raw.v, av = valid ? raw.a : z, bv = valid ? raw.b : z;
+  uint32_t wv[P], kv[P], av[P], bv[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    wv[i] = valid ? raw.w[i] : 0u;
+    kv[i] = valid ? raw.k[i] : 0u;
+    av[i] = valid ? raw.a[i] : 0u;
+    bv[i] = valid ? raw.b[i] : 0u;
+  }
   constexpr float kLog2e = 1.4426950408889634f;
-  float A_[4], R_[4], B_[4], K_[4], eh[4];
+  float A_[kChan], R_[kChan], B_[kChan], K_[kChan], eh[kChan];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const float G = row_prefix_sum(elem4(wv, m) * kLog2e);  // log2 decay through token t
+  for (int m = 0; m < kChan; ++m) {
+    const float G = row_prefix_sum(elem(wv, m) * kLog2e);  // log2 decay through token t
     eh[m] = __builtin_amdgcn_exp2f(G);
-    const float ex = row_prev(eh[m], 1.f);                  // decay through token t-1
+    const float ex = row_prev(eh[m], 1.f);                 // decay through token t-1
     const float ie = __builtin_amdgcn_exp2f(-G);
-    A_[m] = elem4(av, m) * ex;
-    R_[m] = elem4(rv, m) * scale * eh[m];
-    B_[m] = elem4(bv, m) * ie;
-    K_[m] = elem4(kv, m) * ie;
+    A_[m] = elem(av, m) * ex;
+    R_[m] = elem(raw.r, m) * scale * eh[m];
+    B_[m] = elem(bv, m) * ie;
+    K_[m] = elem(kv, m) * ie;
   }
-  uint2 ah, al, rh, rl, bh, bl, kh, kl;
-  split2(A_[0], A_[1], ah.x, al.x);
-  split2(A_[2], A_[3], ah.y, al.y);
-  split2(R_[0], R_[1], rh.x, rl.x);
-  split2(R_[2], R_[3], rh.y, rl.y);
-  split2(B_[0], B_[1], bh.x, bl.x);
-  split2(B_[2], B_[3], bh.y, bl.y);
-  split2(K_[0], K_[1], kh.x, kl.x);
-  split2(K_[2], K_[3], kh.y, kl.y);
-
-  const int c0 = 16 * part + 4 * cg;       // key channels c0 .. c0+3 (consecutive key_pos)
-  const int ro = t * kPR + key_pos(c0);
-  *reinterpret_cast<uint2*>(&S.A[0][ro]) = ah;
-  *reinterpret_cast<uint2*>(&S.A[1][ro]) = al;
-  *reinterpret_cast<uint2*>(&S.R[0][ro]) = rh;
-  *reinterpret_cast<uint2*>(&S.R[1][ro]) = rl;
-  *reinterpret_cast<uint2*>(&sm.Bs[j & 1][0][ro]) = bh;
-  *reinterpret_cast<uint2*>(&sm.Bs[j & 1][1][ro]) = bl;
-  *reinterpret_cast<uint2*>(&sm.Ks[j & 1][0][ro]) = kh;
-  *reinterpret_cast<uint2*>(&sm.Ks[j & 1][1][ro]) = kl;
+  uint32_t ah[P], al[P], rh[P], rl[P], bh[P], bl[P], kh[P], kl[P];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int to = (c0 + m) * kPQ + 8 * (t >> 2) + (t & 3);
-    S.BT[to] = bits4(bh, m);
-    S.BT[to + 4] = bits4(bl, m);
-    S.KT[to] = bits4(kh, m);
-    S.KT[to + 4] = bits4(kl, m);
-    S.VT[to] = bits4(vv, m);
-    S.VT[to + 4] = bits4(vv, m);
+  for (int i = 0; i < P; ++i) {
+    split2(A_[2 * i], A_[2 * i + 1], ah[i], al[i]);
+    split2(R_[2 * i], R_[2 * i + 1], rh[i], rl[i]);
+    split2(B_[2 * i], B_[2 * i + 1], bh[i], bl[i]);
+    split2(K_[2 * i], K_[2 * i + 1], kh[i], kl[i]);
   }
-  *reinterpret_cast<float4*>(&S.gam[t][c0]) = make_float4(eh[0], eh[1], eh[2], eh[3]);
+
+  const int c0 = kChan * (4 * part + cg);  // key channels c0 .. c0+kChan-1 (consecutive key_pos)
+  const int ro = t * kPR + key_pos(c0);
+  st_pairs(&S.A[0][ro], ah);
+  st_pairs(&S.A[1][ro], al);
+  st_pairs(&S.R[0][ro], rh);
+  st_pairs(&S.R[1][ro], rl);
+  st_pairs(&sm.Bs[j & 1][0][ro], bh);
+  st_pairs(&sm.Bs[j & 1][1][ro], bl);
+  st_pairs(&sm.Ks[j & 1][0][ro], kh);
+  st_pairs(&sm.Ks[j & 1][1][ro], kl);
+#pragma unroll
+  for (int m = 0; m < kChan; ++m) {
+    const int to = (c0 + m) * kPQ + 8 * (t >> 2) + (t & 3);
+    S.BT[to] = elem_bits(bh, m);
+    S.BT[to + 4] = elem_bits(bl, m);
+    S.KT[to] = elem_bits(kh, m);
+    S.KT[to + 4] = elem_bits(kl, m);
+    S.VT[to] = elem_bits(raw.v, m);
+    S.VT[to + 4] = elem_bits(raw.v, m);
+  }
+  if constexpr (kChan == 4)
+    *reinterpret_cast<float4*>(&S.gam[t][c0]) = make_float4(eh[0], eh[1], eh[2], eh[3]);
+  else
+    *reinterpret_cast<float2*>(&S.gam[t][c0]) = make_float2(eh[0], eh[1]);
 }
 
 // Score matrix `part` of sub-chunk j (0: L_ab, 1: L_ak, 2: M_rb, 3: M_rk) as
@@ -378,15 +409,29 @@ __device__ __forceinline__ void store_y(void* y, const f32x4& Z, int64_t j, cons
                                         int lane, int wave) {
   const int li = lane & 15, lg = lane >> 4;
   const int64_t tok0 = g.t_beg + kSub * j + 4 * lg;
+  const int64_t yo = tok0 * g.tstride + g.hoff + kSub * wave + li;
+  if (g.t_beg + kSub * (j + 1) <= g.t_end) {  // uniform: the whole sub-chunk is real
+    if (kF32Out) {
+      float* yp = static_cast<float*>(y) + yo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yp[r * g.tstride] = Z[r];
+    } else {
+      uint16_t* yp = static_cast<uint16_t*>(y) + yo;
+      const uint32_t p01 = pack_bf16(Z[0], Z[1]), p23 = pack_bf16(Z[2], Z[3]);
+      yp[0] = static_cast<uint16_t>(p01);
+      yp[g.tstride] = static_cast<uint16_t>(p01 >> 16);
+      yp[2 * g.tstride] = static_cast<uint16_t>(p23);
+      yp[3 * g.tstride] = static_cast<uint16_t>(p23 >> 16);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t tok = tok0 + r;
-    if (tok < g.t_end) {
-      const int64_t yo = tok * g.tstride + g.hoff + kSub * wave + li;
+    if (tok0 + r < g.t_end) {
       if (kF32Out)
-        static_cast<float*>(y)[yo] = Z[r];
+        static_cast<float*>(y)[yo + r * g.tstride] = Z[r];
       else
-        static_cast<uint16_t*>(y)[yo] = f32_to_bf16(Z[r]);
+        static_cast<uint16_t*>(y)[yo + r * g.tstride] = f32_to_bf16(Z[r]);
     }
   }
 }
@@ -462,9 +507,9 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
         hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
-  } else if (wave >= 8) {
+  } else if (wave >= 4 + kOpWaves) {
     if (n_sub > 0) {
-      const int part = wave - 8;
+      const int part = wave - 4 - kOpWaves;
       end_tick();
       stage_scores(sm, 0, lane, part);
       end_tick();
