@@ -374,6 +374,53 @@ def bench_mixed(torch, dev, args, launcher):
     return res
 
 
+def bench_decode_graph(torch, dev, args):
+    """Decode step (1.5B shape, 24 layers, 512-slot pool) as eager launches
+    through the Python ops layer vs one replay of the captured HIP graph
+    (wkvm_amd.graph.DecodeGraph), per batch size: where launch overhead
+    matters (small batches) the graph removes it."""
+    from wkvm_amd import ops, synthetic
+    from wkvm_amd.graph import DecodeGraph
+    from wkvm_amd.layout import RWKV7StateLayout
+    from wkvm_amd.state import RWKV7StateBank
+
+    L, H, S = 24, 32, 512
+    layout = RWKV7StateLayout.for_shape("1.5B")
+    bank = RWKV7StateBank(layout, S, device=dev)
+    gdev = synthetic.make_generator(args.seed + 8, dev)
+    res = {}
+    for B in (1, 8, 64, 256):
+        slots = synthetic.active_slots(S, B, synthetic.make_generator(args.seed + 9))
+        xs = [synthetic.order(synthetic.wkv7_vectors((B, H, 64), gdev)) for _ in range(L)]
+        ids, order = ops.decode_plan(slots, S + 1, dev)
+        y = torch.empty((L, B, H, 64), dtype=torch.bfloat16, device=dev)
+
+        def eager():
+            for l in range(L):
+                ops.wkv7_decode_slots(bank.wkv[l], ids, *xs[l], out=y[l], row_order=order)
+
+        dg = DecodeGraph(bank, B)
+        dg.set_slots(slots)
+        dg.set_inputs(xs)
+        times = {}
+        for name, fn in (("eager", eager), ("graph", dg.replay)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            n = 50
+            t0 = time.perf_counter()
+            for _ in range(n):
+                fn()
+            torch.cuda.synchronize()
+            times[name] = 1e6 * (time.perf_counter() - t0) / n
+        res[f"B{B}"] = {"eager_us_per_step": times["eager"], "graph_us_per_step": times["graph"]}
+        log(f"decode step B={B}: eager {times['eager']:.1f} us, graph {times['graph']:.1f} us")
+        del dg, xs, y
+    del bank
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(args):
     """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
     slots of a 512-slot pool) for as many steps as fit ~10 s, at least one."""
@@ -502,6 +549,7 @@ def main() -> int:
     if not args.no_extra:
         extra["fork_decode_7b"] = bench_fork_decode_7b(torch, dev, args, launcher)
         extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)
+        extra["decode_graph"] = bench_decode_graph(torch, dev, args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     line = {
         "metric": "WKV7 decode slot-steps/s + achieved HBM GB/s; chunked-prefill tokens/s",
