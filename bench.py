@@ -421,6 +421,65 @@ def bench_decode_graph(torch, dev, args):
     return res
 
 
+def bench_store(torch, dev, args):
+    """StateStore HOT <-> WARM transfer of one session's state (every layer's
+    wkv and shift rows): one strided DMA per family (wkv7_slot_transfer) vs
+    the reference's Tensor.copy_ of the non-contiguous slot views
+    (wkvm/store.py:130-131, 151-152), same pinned host tensors, same slots."""
+    import statistics
+
+    from wkvm_amd import ops
+    from wkvm_amd.layout import RWKV7StateLayout
+    from wkvm_amd.state import RWKV7StateBank
+
+    res = {}
+    for shape in ("1.5B", "7B"):
+        bank = RWKV7StateBank(RWKV7StateLayout.for_shape(shape), 8, device=dev)
+        bank.wkv.normal_()
+        slot = 5
+        hw = torch.empty(bank.wkv[:, slot].shape, dtype=bank.wkv.dtype, pin_memory=True)
+        hs = torch.empty(bank.shift[:, :, slot].shape, dtype=bank.shift.dtype, pin_memory=True)
+        nbytes = hw.numel() * hw.element_size() + hs.numel() * hs.element_size()
+
+        def ours_save():
+            ops.slot_to_host(bank.wkv, slot, 1, hw)
+            ops.slot_to_host(bank.shift, slot, 2, hs)
+
+        def ours_load():
+            ops.slot_from_host(bank.wkv, slot, 1, hw)
+            ops.slot_from_host(bank.shift, slot, 2, hs)
+
+        def ref_save():
+            hw.copy_(bank.wkv[:, slot], non_blocking=True)
+            hs.copy_(bank.shift[:, :, slot], non_blocking=True)
+
+        def ref_load():
+            bank.wkv[:, slot].copy_(hw, non_blocking=True)
+            bank.shift[:, :, slot].copy_(hs, non_blocking=True)
+
+        out = {"bytes_per_slot": nbytes}
+        for name, fn in (("save", ours_save), ("load", ours_load),
+                         ("ref_save", ref_save), ("ref_load", ref_load)):
+            ts = []
+            for i in range(23):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                if i >= 3:
+                    ts.append(time.perf_counter() - t0)
+            med = statistics.median(ts)
+            out[f"{name}_us"] = 1e6 * med
+            out[f"{name}_gbps"] = nbytes / med / 1e9
+        res[shape] = out
+        log(f"state store {shape}: {nbytes / 2**20:.1f} MiB/slot; save {out['save_us']:.0f} us "
+            f"({out['save_gbps']:.1f} GB/s) vs Tensor.copy_ {out['ref_save_us']:.0f} us; load "
+            f"{out['load_us']:.0f} us ({out['load_gbps']:.1f} GB/s) vs {out['ref_load_us']:.0f} us")
+        del bank, hw, hs
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(args):
     """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
     slots of a 512-slot pool) for as many steps as fit ~10 s, at least one."""
@@ -550,6 +609,7 @@ def main() -> int:
         extra["fork_decode_7b"] = bench_fork_decode_7b(torch, dev, args, launcher)
         extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)
         extra["decode_graph"] = bench_decode_graph(torch, dev, args)
+        extra["state_store"] = bench_store(torch, dev, args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     line = {
         "metric": "WKV7 decode slot-steps/s + achieved HBM GB/s; chunked-prefill tokens/s",

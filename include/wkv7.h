@@ -56,6 +56,9 @@ extern "C" {
 #define WKV7_Y_BF16 0 /* y written as bf16 (round to nearest even) */
 #define WKV7_Y_F32 1  /* y written as fp32 */
 
+#define WKV7_TO_HOST 0   /* wkv7_slot_transfer: device slot rows -> host */
+#define WKV7_FROM_HOST 1 /* wkv7_slot_transfer: host -> device slot rows */
+
 /* ABI version of the loaded library (WKV7_ABI_VERSION at build time). */
 int wkv7_abi_version(void);
 
@@ -154,6 +157,26 @@ int wkv7_slot_copy(void *dst, int64_t dst_outer_stride, int64_t dst_slot_stride,
 int wkv7_slot_zero(void *base, int64_t outer_stride, int64_t slot_stride, int64_t rows,
                    const int32_t *ids, int64_t outer, int64_t row_bytes, int32_t n,
                    void *stream);
+
+/*
+ * Copy one slot's rows of a slot-pool family between device memory and a
+ * dense host buffer, as one strided DMA copy (no kernel, no staging):
+ *     host + o*row_bytes  <->  base + o*outer_stride + slot*slot_stride
+ * for every outer block o < outer (`row_bytes` each; strides in bytes).
+ * direction: WKV7_TO_HOST or WKV7_FROM_HOST. `host` is a host pointer and
+ * must be pinned (hipHostMalloc, torch pin_memory) for the copy to be
+ * asynchronous; it holds the slot's rows densely, [outer][row_bytes], which
+ * is the layout of the reference's WARM tensors (`bank.wkv[:, slot]` is
+ * [L, H, K, V], `bank.shift[:, :, slot]` is [L, 2, D]).
+ * Replaces the HOT <-> WARM copies of StateStore.save (wkvm/store.py:128-131,
+ * D2H of bank.wkv[:, slot] and bank.shift[:, :, slot] into pinned host
+ * tensors) and StateStore.load (wkvm/store.py:151-152, H2D into the slot
+ * views). Returns WKV7_ERR_ARG for a slot outside [0, rows) or a bad
+ * direction, WKV7_ERR_SHAPE if row_bytes exceeds a stride.
+ */
+int wkv7_slot_transfer(int32_t direction, void *host, void *base, int64_t outer_stride,
+                       int64_t slot_stride, int64_t rows, int32_t slot, int64_t outer,
+                       int64_t row_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -95,6 +95,14 @@ def test_abi_rejects_bad_arguments_before_any_launch():
     assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, dummy, 0, 32, 4, None, 1, 64, 1,
                               None) == _lib.WKV7_ERR_SHAPE
     assert lib.wkv7_slot_zero(None, 0, 64, 4, dummy, 1, 64, 1, None) == _lib.WKV7_ERR_ARG
+    # slot transfer: bad direction, slot out of range, null host, row wider than a stride
+    assert lib.wkv7_slot_transfer(2, dummy, dummy, 256, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 4, 2, 64, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, -1, 2, 64, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(1, None, dummy, 256, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 32, 4, 1, 2, 64, None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 32, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 1, 0, 64, None) == _lib.WKV7_OK
     for code in (_lib.WKV7_ERR_ARG, _lib.WKV7_ERR_SHAPE, _lib.WKV7_ERR_WORKSPACE):
         assert _lib.strerror(code)
 

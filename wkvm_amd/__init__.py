@@ -12,6 +12,10 @@ reference's slot-tensor layout and op signatures:
   ``slot_zero`` -- slot-indexed kernels
 * ``fused_recurrent_rwkv7`` / ``chunk_rwkv7`` -- the fla wkv-op signatures the
   reference's model layer calls
+* ``DecodeGraph`` -- a decode step's WKV launches captured as one HIP graph
+  (the role of experiments/m2_engine_bench.py GraphedDecode)
+* ``StateStore`` -- HOT/WARM/COLD state handles, wkvm/store.py, with the
+  HOT <-> WARM copies as strided DMA transfers
 """
 
 from .layout import HEAD_SIZE, WKV_DTYPE, ModelStateSpec, RWKV7StateLayout, StateFamilySpec
@@ -23,12 +27,15 @@ from .ops import (
     wkv7_decode_slots,
     wkv7_prefill_varlen,
 )
+from .graph import DecodeGraph
 from .runner import WKV7Runner
 from .state import RWKV7StateBank, SlotCache
+from .store import FingerprintMismatch, StateRecord, StateStore
 
 __all__ = [
     "HEAD_SIZE", "WKV_DTYPE", "ModelStateSpec", "RWKV7StateLayout", "StateFamilySpec",
-    "RWKV7StateBank", "SlotCache", "WKV7Runner",
+    "RWKV7StateBank", "SlotCache", "WKV7Runner", "DecodeGraph",
+    "StateStore", "StateRecord", "FingerprintMismatch",
     "wkv7_decode_slots", "wkv7_prefill_varlen", "slot_copy", "slot_zero",
     "chunk_rwkv7", "fused_recurrent_rwkv7",
 ]

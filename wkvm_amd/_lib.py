@@ -22,6 +22,8 @@ WKV7_ERR_SHAPE = -2
 WKV7_ERR_WORKSPACE = -3
 WKV7_Y_BF16 = 0
 WKV7_Y_F32 = 1
+WKV7_TO_HOST = 0
+WKV7_FROM_HOST = 1
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -42,6 +44,7 @@ SIGNATURES = {
     "wkv7_slot_copy": (ctypes.c_int, [
         _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
     "wkv7_slot_zero": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
+    "wkv7_slot_transfer": (ctypes.c_int, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _i64, _i64, _vp]),
 }
 
 _lib = None

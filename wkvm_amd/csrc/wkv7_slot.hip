@@ -150,3 +150,26 @@ extern "C" int wkv7_slot_zero(void* base, int64_t outer_stride, int64_t slot_str
                         uint64_t(slot_stride) | uint64_t(row_bytes);
   return launch_rows<true>(m, row_bytes, n, vector_bytes(bits), as_stream(stream));
 }
+
+extern "C" int wkv7_slot_transfer(int32_t direction, void* host, void* base, int64_t outer_stride,
+                                  int64_t slot_stride, int64_t rows, int32_t slot, int64_t outer,
+                                  int64_t row_bytes, void* stream) {
+  if (direction != WKV7_TO_HOST && direction != WKV7_FROM_HOST) return WKV7_ERR_ARG;
+  if (outer < 0 || row_bytes < 0 || rows < 1 || slot < 0 || slot >= rows) return WKV7_ERR_ARG;
+  if (outer == 0 || row_bytes == 0) return WKV7_OK;
+  if (!host || !base) return WKV7_ERR_ARG;
+  if (rows > 1 && row_bytes > slot_stride) return WKV7_ERR_SHAPE;
+  if (outer > 1 && row_bytes > outer_stride) return WKV7_ERR_SHAPE;
+  char* dev = static_cast<char*>(base) + int64_t(slot) * slot_stride;
+  const size_t width = size_t(row_bytes), height = size_t(outer);
+  // a single block needs no pitch; give the DMA its own width then
+  const size_t dev_pitch = outer > 1 ? size_t(outer_stride) : width;
+  hipError_t e;
+  if (direction == WKV7_TO_HOST)
+    e = hipMemcpy2DAsync(host, width, dev, dev_pitch, width, height, hipMemcpyDeviceToHost,
+                         as_stream(stream));
+  else
+    e = hipMemcpy2DAsync(dev, dev_pitch, host, width, width, height, hipMemcpyHostToDevice,
+                         as_stream(stream));
+  return e == hipSuccess ? WKV7_OK : static_cast<int>(e);
+}

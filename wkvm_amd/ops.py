@@ -318,6 +318,44 @@ def slot_copy(dst: torch.Tensor, dst_ids, src: torch.Tensor, src_ids, slot_dim: 
     _lib.check(rc, "wkv7_slot_copy")
 
 
+def _slot_transfer(direction: int, t: torch.Tensor, slot: int, slot_dim: int,
+                   host: torch.Tensor) -> None:
+    _require_cuda(t, "slot tensor")
+    outer, outer_stride, slot_stride, rows, row_bytes = slot_view(t, slot_dim)
+    if not 0 <= int(slot) < rows:
+        raise ValueError(f"slot {slot} out of range [0, {rows})")
+    if host.is_cuda or not host.is_contiguous() or host.dtype != t.dtype:
+        raise ValueError("host buffer must be a contiguous CPU tensor of the slot tensor's dtype")
+    if host.numel() * host.element_size() != outer * row_bytes:
+        raise ValueError(f"host buffer holds {host.numel() * host.element_size()} B, "
+                         f"the slot's rows are {outer * row_bytes} B")
+    if not host.is_pinned():
+        raise ValueError("host buffer must be pinned (pin_memory) for the DMA copy")
+    rc = _lib.load().wkv7_slot_transfer(direction, host.data_ptr(), t.data_ptr(), outer_stride,
+                                        slot_stride, rows, int(slot), outer, row_bytes,
+                                        _stream_ptr(t.device))
+    _lib.check(rc, "wkv7_slot_transfer")
+
+
+def slot_to_host(t: torch.Tensor, slot: int, slot_dim: int, host: torch.Tensor | None = None,
+                 ) -> torch.Tensor:
+    """Asynchronous DMA of one slot's rows of ``t`` (every outer block) into a
+    dense pinned host tensor shaped like ``t.select(slot_dim, slot)``; the
+    caller synchronises before reading it."""
+    _require_cuda(t, "slot tensor")
+    shape = t.shape[:slot_dim] + t.shape[slot_dim + 1:]
+    if host is None:
+        host = torch.empty(shape, dtype=t.dtype, pin_memory=True)
+    _slot_transfer(_lib.WKV7_TO_HOST, t, slot, slot_dim, host)
+    return host
+
+
+def slot_from_host(t: torch.Tensor, slot: int, slot_dim: int, host: torch.Tensor) -> None:
+    """Asynchronous DMA of a dense pinned host tensor (shaped like
+    ``t.select(slot_dim, slot)``) into one slot's rows of ``t``."""
+    _slot_transfer(_lib.WKV7_FROM_HOST, t, slot, slot_dim, host)
+
+
 def _overlaps(x: torch.Tensor, y: torch.Tensor) -> bool:
     return x.untyped_storage().data_ptr() == y.untyped_storage().data_ptr()
 
