@@ -19,9 +19,9 @@
 //
 // Schedule: a four-deep software pipeline over sub-chunks, one workgroup
 // barrier per tick. In tick k four state waves run sub-chunk k's state step
-// (the products above, 16 value columns each) while eight more waves prepare
-// the sub-chunks ahead:
+// (the products above, 16 value columns each) and
 //   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
+// while eight more waves prepare the sub-chunks further ahead:
 //   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
 //                              per wave
@@ -454,12 +454,12 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
 }
 
 // Twelve wavefronts in three kinds: waves 0-3 run the state chain (wave q
-// owns value columns [16q, 16q+16)); waves 4-7 build operands (part p =
-// wave - 4 handles key channels [16p, 16p+16)); waves 8-11 compute score
-// matrix p and T columns [4p, 4p+4) (p = wave - 8). Each SIMD holds one wave
-// of each kind, so the hardware interleaves the state chain's MFMA latencies
-// with the operand and inverse work. All kinds pass the same sequence of
-// barriers: three fill ticks, then one per sub-chunk.
+// owns value columns [16q, 16q+16)) and T columns [4q, 4q+4) of the next
+// sub-chunk; waves 4-7 build operands (part p = wave - 4 handles key channels
+// [16p, 16p+16)); waves 8-11 compute score matrix p = wave - 8. Each SIMD
+// holds one wave of each kind, so the hardware interleaves the state chain's
+// MFMA latencies with the operand and score work. All kinds pass the same
+// sequence of barriers: three fill ticks, then one per sub-chunk.
 template <bool kF32Out>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
@@ -495,9 +495,11 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     if (n_sub > 0) {
       end_tick();  // fill ticks
       end_tick();
+      stage_inverse(sm, 0, lane, wave);
       end_tick();
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
+        stage_inverse(sm, k + 1, lane, wave);
         store_y<kF32Out>(y, yv, k, g, lane, wave);
         end_tick();
       }
@@ -514,10 +516,8 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       stage_scores(sm, 0, lane, part);
       end_tick();
       stage_scores(sm, 1, lane, part);
-      stage_inverse(sm, 0, lane, part);
       end_tick();
       for (int64_t k = 0; k < n_sub; ++k) {
-        stage_inverse(sm, k + 1, lane, part);
         stage_scores(sm, k + 2, lane, part);
         end_tick();
       }
