@@ -79,9 +79,10 @@ class Launcher:
         if rc:
             self.check(rc, "wkv7_decode_slots")
 
-    def prefill(self, pool, rows, H, ids, cu, nseq, T, xs, y, zero_init, ws=None, ws_bytes=0):
-        rc = self.lib.wkv7_prefill_varlen(pool, rows, H, ids, cu, nseq, T, *xs, y, 0, zero_init,
-                                          1.0, ws, ws_bytes, self.stream)
+    def prefill(self, pool, rows, H, ids, cu, nseq, T, xs, y, zero_init, ws=None, ws_bytes=0,
+                order=None):
+        rc = self.lib.wkv7_prefill_varlen(pool, rows, H, ids, cu, order, nseq, T, *xs, y, 0,
+                                          zero_init, 1.0, ws, ws_bytes, self.stream)
         if rc:
             self.check(rc, "wkv7_prefill_varlen")
 
@@ -334,6 +335,7 @@ def bench_mixed(torch, dev, args, launcher):
     dec_t = torch.tensor(dec, dtype=torch.int32, device=dev)
     dec_order = sorted_order(torch, dec, dev)
     cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    lpt_t = torch.tensor(ops.longest_first(cu), dtype=torch.int32, device=dev)
     dx = [synthetic.order(synthetic.wkv7_vectors((ND, H, 64), gdev)) for _ in range(L)]
     px = [synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev)) for _ in range(2)]
     dy = torch.empty((ND, H, 64), dtype=torch.bfloat16, device=dev)
@@ -342,33 +344,41 @@ def bench_mixed(torch, dev, args, launcher):
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     ws_ptr = ws.data_ptr() if ws_bytes else None
 
-    def step():
+    def step(order=lpt_t.data_ptr(), decode=True):
         for l in range(L):
-            launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(), dec_order.data_ptr(), ND,
-                            ptrs(dx[l]),
-                            dy.data_ptr())
+            if decode:
+                launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(),
+                                dec_order.data_ptr(), ND, ptrs(dx[l]), dy.data_ptr())
             launcher.prefill(wkv[l].data_ptr(), S + 1, H, pre_t.data_ptr(), cu_t.data_ptr(), NP, T,
-                             ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes)
+                             ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes, order)
+
+    def timed(**kw):
+        reps = 3
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            step(**kw)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
 
     step()
     torch.cuda.synchronize()
-    reps = 3
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    ms = timed()
+    # the ragged prefill alone, longest-first vs index order of the sequences
+    pre_lpt, pre_idx = timed(decode=False), timed(decode=False, order=None)
     step_bytes = L * (ND * slot_layer_bytes(H) + T * H * 7 * HEAD_VEC_B + NP * H * HEAD_STATE_B)
     res = {
         "ms_per_step": ms,
         "prefill_tokens": T,
         "hbm_gbps": step_bytes / (ms * 1e-3) / 1e9,
         "tokens_per_s": (T + ND) / (ms * 1e-3),
+        "prefill_ms_longest_first": pre_lpt,
+        "prefill_ms_index_order": pre_idx,
     }
     log(f"mixed cfg4: {ms:.2f} ms/step over 24 layers, {T} prefill tokens + {ND} decodes, "
-        f"{res['hbm_gbps']:.0f} GB/s")
+        f"{res['hbm_gbps']:.0f} GB/s; prefill alone {pre_lpt:.2f} ms longest-first, "
+        f"{pre_idx:.2f} ms index order")
     del wkv, dx, px, dy, py, ws
     torch.cuda.empty_cache()
     return res

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 1
+#define WKV7_ABI_VERSION 2
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -107,6 +107,11 @@ int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
  *   slot_ids      [nseq] int32 (device), distinct
  *   cu_seqlens    [nseq + 1] int32 (device), cu_seqlens[0] = 0,
  *                 non-decreasing, cu_seqlens[nseq] = total_tokens
+ *   seq_order     [nseq] int32 (device) or NULL: the order in which the
+ *                 sequences are started (a permutation of 0..nseq-1; NULL =
+ *                 0..nseq-1). Longest first packs ragged batches onto the
+ *                 compute units with the least idle tail; results do not
+ *                 depend on it
  *   r..b          [total_tokens, H, 64] bf16, 16-byte aligned (else WKV7_ERR_SHAPE)
  *   y             [total_tokens, H, 64], dtype per y_dtype
  *   workspace     device scratch of at least
@@ -115,7 +120,7 @@ int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
  */
 int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
                         const int32_t *slot_ids, const int32_t *cu_seqlens,
-                        int32_t nseq, int64_t total_tokens,
+                        const int32_t *seq_order, int32_t nseq, int64_t total_tokens,
                         const uint16_t *r, const uint16_t *w, const uint16_t *k,
                         const uint16_t *v, const uint16_t *a, const uint16_t *b,
                         void *y, int32_t y_dtype, int32_t zero_init, float scale,

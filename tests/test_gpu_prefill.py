@@ -69,6 +69,35 @@ def test_ragged_lengths_from_slot_state(dev, zero_init, y_dtype):
         assert torch.equal(gpool[ids[2]].cpu(), pool[ids[2]])
 
 
+def test_sequence_order_changes_nothing(dev):
+    """The visiting order of the sequences (``seq_order``) only schedules the
+    workgroups: identity, reversed and longest-first launches give the same
+    bytes, final states and y alike."""
+    H, S = 4, 10
+    lens = [3, 300, 0, 64, 129, 17, 640]
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    gen = synthetic.make_generator(33)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = synthetic.active_slots(S, len(lens), gen)
+    vecs = [x.to(dev) for x in synthetic.order(synthetic.wkv7_vectors((cu[-1], H, 64), gen))]
+    n = len(lens)
+    orders = [None, list(range(n)), list(range(n))[::-1], ops.longest_first(cu)]
+    assert ops.longest_first(cu)[:2] == [6, 1]
+    outs = []
+    for order in orders:
+        gpool = pool.to(dev)
+        seq = None if order is None else torch.tensor(order, dtype=torch.int32, device=dev)
+        y = ops.wkv7_prefill_varlen(gpool, ids, cu, *vecs, seq_order=seq)
+        torch.cuda.synchronize()
+        outs.append((gpool.cpu(), y.cpu()))
+    for p, y in outs[1:]:
+        assert torch.equal(p, outs[0][0]) and torch.equal(y, outs[0][1])
+    with pytest.raises(ValueError):
+        ops.wkv7_prefill_varlen(pool.to(dev), ids, cu, *vecs,
+                                seq_order=torch.arange(n - 1, dtype=torch.int32, device=dev))
+
+
 def test_cfg2_full_size_zero_init(dev):
     """Config 2: 1.5B shape (H=32), 8 sequences x 4096 tokens from zero state,
     final states written to 8 seeded slots of a 16-slot pool; every token's y

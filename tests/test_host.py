@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 1
+    assert lib.wkv7_abi_version() == 2
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():
@@ -83,10 +83,10 @@ def test_abi_rejects_bad_arguments_before_any_launch():
     assert lib.wkv7_decode_slots(dummy, 5, 0, dummy, None, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
     assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, None, 0, *six, dummy, 0, 1.0, None) == _lib.WKV7_OK
     # prefill: negative sizes, missing cu_seqlens
-    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, dummy, -1, 0, *six, dummy, 0, 0, 1.0,
-                                   None, 0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, None, 1, 4, *six, dummy, 0, 0, 1.0,
-                                   None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, dummy, None, -1, 0, *six, dummy, 0, 0,
+                                   1.0, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, None, None, 1, 4, *six, dummy, 0, 0,
+                                   1.0, None, 0, None) == _lib.WKV7_ERR_ARG
     # slot copy: negative count, null src, row wider than the slot stride
     assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, dummy, 0, 64, 4, None, 1, 64, -1,
                               None) == _lib.WKV7_ERR_ARG
@@ -149,6 +149,12 @@ def test_host_cu_validation():
     for bad in ([1, 7], [0, 5], [0, 4, 3, 7], []):
         with pytest.raises(ValueError):
             ops._host_cu(bad, 7)
+
+
+def test_longest_first_order():
+    # lengths 3, 0, 9, 3, 5: longest first, equal lengths in index order
+    assert ops.longest_first([0, 3, 3, 12, 15, 20]) == [2, 4, 0, 3, 1]
+    assert ops.longest_first([0]) == []
 
 
 def test_slot_view_describes_bank_tensors():

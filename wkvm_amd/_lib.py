@@ -38,8 +38,8 @@ SIGNATURES = {
     "wkv7_decode_slots": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _f32, _vp]),
     "wkv7_prefill_varlen": (ctypes.c_int, [
-        _vp, _i64, _i32, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
-        _f32, _vp, _sz, _vp]),
+        _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+        _i32, _f32, _vp, _sz, _vp]),
     "wkv7_prefill_workspace_bytes": (_sz, [_i32, _i32, _i64]),
     "wkv7_slot_copy": (ctypes.c_int, [
         _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),

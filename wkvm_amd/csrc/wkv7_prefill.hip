@@ -463,14 +463,16 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
 template <bool kF32Out>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu_seqlens, Inputs in, void* __restrict__ y,
-    int64_t total_tokens, int zero_init, float scale) {
+    const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ seq_order, int nseq,
+    Inputs in, void* __restrict__ y, int64_t total_tokens, int zero_init, float scale) {
   __shared__ Shared sm;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t seq = blockIdx.x / H;
-  const int64_t head = blockIdx.x - seq * H;
+  const int64_t pos = blockIdx.x / H;
+  const int64_t head = blockIdx.x - pos * H;
+  const int64_t seq = seq_order ? int64_t(seq_order[pos]) : pos;
+  if (seq < 0 || seq >= nseq) return;  // uniform: the whole block leaves
   const int64_t slot = slot_ids[seq];
   if (slot < 0 || slot >= num_rows) return;  // uniform: the whole block leaves
   SeqGeom g;
@@ -567,7 +569,8 @@ extern "C" size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t 
 
 extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H,
                                    const int32_t* slot_ids, const int32_t* cu_seqlens,
-                                   int32_t nseq, int64_t total_tokens, const uint16_t* r,
+                                   const int32_t* seq_order, int32_t nseq, int64_t total_tokens,
+                                   const uint16_t* r,
                                    const uint16_t* w, const uint16_t* k, const uint16_t* v,
                                    const uint16_t* a, const uint16_t* b, void* y, int32_t y_dtype,
                                    int32_t zero_init, float scale, void* workspace,
@@ -590,9 +593,11 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
   const Inputs in{r, w, k, v, a, b};
   if (y_dtype == WKV7_Y_F32)
     prefill_chunked_kernel<true><<<unsigned(blocks), kThreads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, cu_seqlens, in, y, total_tokens, zero_init, scale);
+        wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq, in, y, total_tokens,
+        zero_init, scale);
   else
     prefill_chunked_kernel<false><<<unsigned(blocks), kThreads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, cu_seqlens, in, y, total_tokens, zero_init, scale);
+        wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq, in, y, total_tokens,
+        zero_init, scale);
   return launch_status();
 }

@@ -191,15 +191,26 @@ def prefill_workspace_bytes(H: int, nseq: int, total_tokens: int) -> int:
     return int(_lib.load().wkv7_prefill_workspace_bytes(int(H), int(nseq), int(total_tokens)))
 
 
+def longest_first(cu: Sequence[int]) -> list[int]:
+    """Sequence order for a ragged prefill launch: longest first (ties in
+    index order), which packs the per-(sequence, head) workgroups onto the
+    compute units with the smallest idle tail."""
+    n = len(cu) - 1
+    return sorted(range(n), key=lambda s: cu[s] - cu[s + 1])
+
+
 def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, v, a, b, *,
                         zero_init: bool = False, scale: float = 1.0,
                         out: torch.Tensor | None = None,
                         out_dtype: torch.dtype = torch.bfloat16,
-                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+                        workspace: torch.Tensor | None = None,
+                        seq_order: torch.Tensor | None = None) -> torch.Tensor:
     """Ragged prefill: sequence ``s`` runs tokens ``cu_seqlens[s]:cu_seqlens[s+1]``
     of the ``[T, H, 64]`` bf16 inputs from slot ``slot_ids[s]`` (or zero state
     if ``zero_init``) and leaves its final state in that slot. Returns ``y``
-    ``[T, H, 64]``.
+    ``[T, H, 64]``. ``seq_order`` (device int32 permutation) only sets the
+    order in which sequences are started; for host ``cu_seqlens`` it is
+    computed here (longest first).
     """
     rows, H = _check_pool(wkv_layer)
     dev = wkv_layer.device
@@ -216,7 +227,14 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
         lst = _host_cu(cu_seqlens, T)
         if len(lst) != nseq + 1:
             raise ValueError(f"cu_seqlens has {len(lst)} entries for {nseq} sequences")
-        cu = torch.tensor(lst, dtype=torch.int32, device=dev)
+        both = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
+        cu = both[:nseq + 1]
+        if seq_order is None:
+            seq_order = both[nseq + 1:]
+    if seq_order is not None:
+        if not (isinstance(seq_order, torch.Tensor) and seq_order.is_cuda
+                and seq_order.dtype == torch.int32 and seq_order.shape == (nseq,)):
+            raise ValueError("seq_order must be a device int32 tensor of nseq entries")
     code = _y_code(out.dtype if out is not None else out_dtype)
     y = _out(out, (T, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
     if nseq == 0:
@@ -230,8 +248,9 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
             raise ValueError(f"workspace needs {need} bytes")
     ws_ptr = workspace.data_ptr() if (workspace is not None and need > 0) else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
-    rc = lib.wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), cu.data_ptr(), nseq,
-                                 T, *[x.data_ptr() for x in xs], y.data_ptr(), code,
+    rc = lib.wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), cu.data_ptr(),
+                                 _ptr(seq_order), nseq, T, *[x.data_ptr() for x in xs],
+                                 y.data_ptr(), code,
                                  int(bool(zero_init)), float(scale), ws_ptr, ws_bytes,
                                  _stream_ptr(dev))
     _lib.check(rc, "wkv7_prefill_varlen")
