@@ -468,17 +468,22 @@ def bench_store(torch, dev, args):
             bank.shift[:, :, slot].copy_(hs, non_blocking=True)
 
         out = {"bytes_per_slot": nbytes}
-        for name, fn in (("save", ours_save), ("load", ours_load),
-                         ("ref_save", ref_save), ("ref_load", ref_load)):
-            ts = []
-            for i in range(23):
+        fns = (("save", ours_save), ("load", ours_load), ("ref_save", ref_save),
+               ("ref_load", ref_load))
+        # The host link runs slower for the first milliseconds of traffic after
+        # GPU-only work, so every variant is warmed up and then timed in
+        # interleaved rounds: all of them see the same link state.
+        ts = {name: [] for name, _ in fns}
+        for i in range(30):
+            for name, fn in fns:
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 fn()
                 torch.cuda.synchronize()
-                if i >= 3:
-                    ts.append(time.perf_counter() - t0)
-            med = statistics.median(ts)
+                if i >= 10:
+                    ts[name].append(time.perf_counter() - t0)
+        for name, _ in fns:
+            med = statistics.median(ts[name])
             out[f"{name}_us"] = 1e6 * med
             out[f"{name}_gbps"] = nbytes / med / 1e9
         res[shape] = out
