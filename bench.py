@@ -433,9 +433,12 @@ def bench_decode_graph(torch, dev, args):
 
 def bench_store(torch, dev, args):
     """StateStore HOT <-> WARM transfer of one session's state (every layer's
-    wkv and shift rows): one strided DMA per family (wkv7_slot_transfer) vs
-    the reference's Tensor.copy_ of the non-contiguous slot views
-    (wkvm/store.py:130-131, 151-152), same pinned host tensors, same slots."""
+    wkv and shift rows), vs the reference's Tensor.copy_ of the non-contiguous
+    slot views (wkvm/store.py:130-131, 151-152), same pinned host tensors, same
+    slots. ``save`` is the StateStore path (both families gathered into a
+    device staging buffer by wkv7_slot_copy, then one contiguous DMA each);
+    ``save_strided`` is wkv7_slot_transfer's 2-D DMA; ``load`` is
+    wkv7_slot_transfer's 2-D DMA, the StateStore load path."""
     import statistics
 
     from wkvm_amd import ops
@@ -449,13 +452,23 @@ def bench_store(torch, dev, args):
         slot = 5
         hw = torch.empty(bank.wkv[:, slot].shape, dtype=bank.wkv.dtype, pin_memory=True)
         hs = torch.empty(bank.shift[:, :, slot].shape, dtype=bank.shift.dtype, pin_memory=True)
-        nbytes = hw.numel() * hw.element_size() + hs.numel() * hs.element_size()
+        wb, sb = hw.numel() * hw.element_size(), hs.numel() * hs.element_size()
+        nbytes = wb + sb
+        staging = torch.empty(wb + sb, dtype=torch.uint8, device=dev)
+        stw = staging[:wb].view(hw.dtype).view(hw.shape)
+        sts = staging[wb:].view(hs.dtype).view(hs.shape)
 
-        def ours_save():
+        def save():
+            ops.slot_gather_dense(bank.wkv, slot, 1, stw)
+            ops.slot_gather_dense(bank.shift, slot, 2, sts)
+            hw.copy_(stw, non_blocking=True)
+            hs.copy_(sts, non_blocking=True)
+
+        def save_strided():
             ops.slot_to_host(bank.wkv, slot, 1, hw)
             ops.slot_to_host(bank.shift, slot, 2, hs)
 
-        def ours_load():
+        def load():
             ops.slot_from_host(bank.wkv, slot, 1, hw)
             ops.slot_from_host(bank.shift, slot, 2, hs)
 
@@ -468,13 +481,13 @@ def bench_store(torch, dev, args):
             bank.shift[:, :, slot].copy_(hs, non_blocking=True)
 
         out = {"bytes_per_slot": nbytes}
-        fns = (("save", ours_save), ("load", ours_load), ("ref_save", ref_save),
-               ("ref_load", ref_load))
+        fns = (("save", save), ("save_strided", save_strided), ("load", load),
+               ("ref_save", ref_save), ("ref_load", ref_load))
         # The host link runs slower for the first milliseconds of traffic after
         # GPU-only work, so every variant is warmed up and then timed in
         # interleaved rounds: all of them see the same link state.
         ts = {name: [] for name, _ in fns}
-        for i in range(30):
+        for i in range(40):
             for name, fn in fns:
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
@@ -488,9 +501,10 @@ def bench_store(torch, dev, args):
             out[f"{name}_gbps"] = nbytes / med / 1e9
         res[shape] = out
         log(f"state store {shape}: {nbytes / 2**20:.1f} MiB/slot; save {out['save_us']:.0f} us "
-            f"({out['save_gbps']:.1f} GB/s) vs Tensor.copy_ {out['ref_save_us']:.0f} us; load "
-            f"{out['load_us']:.0f} us ({out['load_gbps']:.1f} GB/s) vs {out['ref_load_us']:.0f} us")
-        del bank, hw, hs
+            f"({out['save_gbps']:.1f} GB/s; strided DMA {out['save_strided_us']:.0f} us) vs "
+            f"Tensor.copy_ {out['ref_save_us']:.0f} us; load {out['load_us']:.0f} us "
+            f"({out['load_gbps']:.1f} GB/s) vs Tensor.copy_ {out['ref_load_us']:.0f} us")
+        del bank, hw, hs, staging, stw, sts
         torch.cuda.empty_cache()
     return res
 

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 2
+#define WKV7_ABI_VERSION 3
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -165,9 +165,15 @@ int wkv7_slot_zero(void *base, int64_t outer_stride, int64_t slot_stride, int64_
 
 /*
  * Copy one slot's rows of a slot-pool family between device memory and a
- * dense host buffer, as one strided DMA copy (no kernel, no staging):
+ * dense host buffer:
  *     host + o*row_bytes  <->  base + o*outer_stride + slot*slot_stride
  * for every outer block o < outer (`row_bytes` each; strides in bytes).
+ * With staging == NULL the copy is one strided DMA (no kernel). With a
+ * device staging buffer of at least outer*row_bytes bytes, the slot's rows
+ * are gathered into (or scattered from) it by the copy kernel and the host
+ * side moves as one contiguous DMA; strided device-to-host DMA runs at half
+ * the host link's rate on some MI355X boxes, the contiguous one does not.
+ * A staging buffer smaller than outer*row_bytes is WKV7_ERR_WORKSPACE.
  * direction: WKV7_TO_HOST or WKV7_FROM_HOST. `host` is a host pointer and
  * must be pinned (hipHostMalloc, torch pin_memory) for the copy to be
  * asynchronous; it holds the slot's rows densely, [outer][row_bytes], which
@@ -181,7 +187,7 @@ int wkv7_slot_zero(void *base, int64_t outer_stride, int64_t slot_stride, int64_
  */
 int wkv7_slot_transfer(int32_t direction, void *host, void *base, int64_t outer_stride,
                        int64_t slot_stride, int64_t rows, int32_t slot, int64_t outer,
-                       int64_t row_bytes, void *stream);
+                       int64_t row_bytes, void *staging, size_t staging_bytes, void *stream);
 
 #ifdef __cplusplus
 }

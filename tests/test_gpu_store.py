@@ -102,3 +102,37 @@ def test_rejected_load_moves_nothing(dev, tmp_path):
         ops.slot_from_host(bank.wkv, bank.num_slots + 1, 1, st._tensors(h)["wkv"])
     torch.cuda.synchronize()
     assert torch.equal(bank.wkv, before_w) and torch.equal(bank.shift, before_s)
+
+
+@pytest.mark.parametrize("staged", [False, True])
+def test_transfer_paths_bit_exact(dev, staged):
+    """Both transfer paths (strided DMA; device gather/scatter through a
+    staging buffer plus a contiguous DMA) move exactly the slot view's bytes,
+    for fp32 rows, bf16 rows and rows whose size allows only 2-byte vectors."""
+    g = synthetic.make_generator(5, dev)
+    cases = [(torch.randn(3, 7, 4, 64, 64, device=dev, generator=g), 1),
+             (torch.randn(2, 2, 9, 96, device=dev, generator=g).to(torch.bfloat16), 2),
+             (torch.randn(4, 5, 33, device=dev, generator=g).to(torch.bfloat16), 1)]
+    for t, dim in cases:
+        slot = t.shape[dim] - 2
+        view = t.select(dim, slot)
+        nbytes = view.numel() * t.element_size()
+        staging = torch.empty(nbytes + 64, dtype=torch.uint8, device=dev) if staged else None
+        host = ops.slot_to_host(t, slot, dim, staging=staging)
+        dense = torch.empty(view.shape, dtype=t.dtype, device=dev)
+        ops.slot_gather_dense(t, slot, dim, dense)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(host, view.cpu())
+        assert torch.equal(dense, view)
+        before = t.clone()
+        src = torch.randn(view.shape, generator=torch.Generator().manual_seed(1)).to(t.dtype)
+        src = src.pin_memory()
+        ops.slot_from_host(t, 1, dim, src, staging=staging)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(t.select(dim, 1).cpu(), src)
+        keep = [i for i in range(t.shape[dim]) if i != 1]
+        assert torch.equal(t.index_select(dim, torch.tensor(keep, device=dev)),
+                           before.index_select(dim, torch.tensor(keep, device=dev)))
+    small = torch.empty(16, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        ops.slot_to_host(cases[0][0], 1, 1, staging=small)

@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 2
+    assert lib.wkv7_abi_version() == 3
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():
@@ -96,13 +96,16 @@ def test_abi_rejects_bad_arguments_before_any_launch():
                               None) == _lib.WKV7_ERR_SHAPE
     assert lib.wkv7_slot_zero(None, 0, 64, 4, dummy, 1, 64, 1, None) == _lib.WKV7_ERR_ARG
     # slot transfer: bad direction, slot out of range, null host, row wider than a stride
-    assert lib.wkv7_slot_transfer(2, dummy, dummy, 256, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 4, 2, 64, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, -1, 2, 64, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_slot_transfer(1, None, dummy, 256, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 32, 4, 1, 2, 64, None) == _lib.WKV7_ERR_SHAPE
-    assert lib.wkv7_slot_transfer(0, dummy, dummy, 32, 64, 4, 1, 2, 64, None) == _lib.WKV7_ERR_SHAPE
-    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 1, 0, 64, None) == _lib.WKV7_OK
+    assert lib.wkv7_slot_transfer(2, dummy, dummy, 256, 64, 4, 1, 2, 64, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 4, 2, 64, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, -1, 2, 64, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(1, None, dummy, 256, 64, 4, 1, 2, 64, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 32, 4, 1, 2, 64, None, 0, None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 32, 64, 4, 1, 2, 64, None, 0, None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 1, 0, 64, None, 0, None) == _lib.WKV7_OK
+    # a staging buffer smaller than the slot's rows (2 x 64 B)
+    assert lib.wkv7_slot_transfer(0, dummy, dummy, 256, 64, 4, 1, 2, 64, dummy, 127,
+                                  None) == _lib.WKV7_ERR_WORKSPACE
     for code in (_lib.WKV7_ERR_ARG, _lib.WKV7_ERR_SHAPE, _lib.WKV7_ERR_WORKSPACE):
         assert _lib.strerror(code)
 

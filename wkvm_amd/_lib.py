@@ -44,7 +44,8 @@ SIGNATURES = {
     "wkv7_slot_copy": (ctypes.c_int, [
         _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
     "wkv7_slot_zero": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
-    "wkv7_slot_transfer": (ctypes.c_int, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _i64, _i64, _vp]),
+    "wkv7_slot_transfer": (ctypes.c_int, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _i64, _i64,
+                                         _vp, _sz, _vp]),
 }
 
 _lib = None

@@ -153,23 +153,45 @@ extern "C" int wkv7_slot_zero(void* base, int64_t outer_stride, int64_t slot_str
 
 extern "C" int wkv7_slot_transfer(int32_t direction, void* host, void* base, int64_t outer_stride,
                                   int64_t slot_stride, int64_t rows, int32_t slot, int64_t outer,
-                                  int64_t row_bytes, void* stream) {
+                                  int64_t row_bytes, void* staging, size_t staging_bytes,
+                                  void* stream) {
   if (direction != WKV7_TO_HOST && direction != WKV7_FROM_HOST) return WKV7_ERR_ARG;
   if (outer < 0 || row_bytes < 0 || rows < 1 || slot < 0 || slot >= rows) return WKV7_ERR_ARG;
   if (outer == 0 || row_bytes == 0) return WKV7_OK;
   if (!host || !base) return WKV7_ERR_ARG;
   if (rows > 1 && row_bytes > slot_stride) return WKV7_ERR_SHAPE;
   if (outer > 1 && row_bytes > outer_stride) return WKV7_ERR_SHAPE;
+  const size_t total = size_t(outer) * size_t(row_bytes);
+  if (staging && staging_bytes < total) return WKV7_ERR_WORKSPACE;
   char* dev = static_cast<char*>(base) + int64_t(slot) * slot_stride;
+  hipStream_t s = as_stream(stream);
+  hipError_t e;
+  if (staging) {
+    // Dense device staging: the slot's strided rows <-> staging with the copy
+    // kernel (HBM speed), then one contiguous DMA to or from the host.
+    char* st = static_cast<char*>(staging);
+    const uint64_t bits = reinterpret_cast<uintptr_t>(dev) | reinterpret_cast<uintptr_t>(st) |
+                          uint64_t(outer_stride) | uint64_t(row_bytes);
+    const int vb = vector_bytes(bits);
+    if (direction == WKV7_TO_HOST) {
+      RowMap m{st, row_bytes, 0, 1, nullptr, dev, outer_stride, 0, 1, nullptr, outer};
+      const int rc = launch_rows<false>(m, row_bytes, 1, vb, s);
+      if (rc != WKV7_OK) return rc;
+      e = hipMemcpyAsync(host, st, total, hipMemcpyDeviceToHost, s);
+    } else {
+      e = hipMemcpyAsync(st, host, total, hipMemcpyHostToDevice, s);
+      if (e != hipSuccess) return static_cast<int>(e);
+      RowMap m{dev, outer_stride, 0, 1, nullptr, st, row_bytes, 0, 1, nullptr, outer};
+      return launch_rows<false>(m, row_bytes, 1, vb, s);
+    }
+    return e == hipSuccess ? WKV7_OK : static_cast<int>(e);
+  }
   const size_t width = size_t(row_bytes), height = size_t(outer);
   // a single block needs no pitch; give the DMA its own width then
   const size_t dev_pitch = outer > 1 ? size_t(outer_stride) : width;
-  hipError_t e;
   if (direction == WKV7_TO_HOST)
-    e = hipMemcpy2DAsync(host, width, dev, dev_pitch, width, height, hipMemcpyDeviceToHost,
-                         as_stream(stream));
+    e = hipMemcpy2DAsync(host, width, dev, dev_pitch, width, height, hipMemcpyDeviceToHost, s);
   else
-    e = hipMemcpy2DAsync(dev, dev_pitch, host, width, width, height, hipMemcpyHostToDevice,
-                         as_stream(stream));
+    e = hipMemcpy2DAsync(dev, dev_pitch, host, width, width, height, hipMemcpyHostToDevice, s);
   return e == hipSuccess ? WKV7_OK : static_cast<int>(e);
 }

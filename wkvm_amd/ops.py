@@ -337,8 +337,27 @@ def slot_copy(dst: torch.Tensor, dst_ids, src: torch.Tensor, src_ids, slot_dim: 
     _lib.check(rc, "wkv7_slot_copy")
 
 
+def slot_gather_dense(t: torch.Tensor, slot: int, slot_dim: int, out: torch.Tensor) -> None:
+    """Bit-exact ``out = t.select(slot_dim, slot)`` into a dense device tensor
+    with one ``wkv7_slot_copy`` launch (no id upload: the slot's rows are
+    addressed directly)."""
+    _require_cuda(t, "slot tensor")
+    outer, outer_stride, slot_stride, rows, row_bytes = slot_view(t, slot_dim)
+    if not 0 <= int(slot) < rows:
+        raise ValueError(f"slot {slot} out of range [0, {rows})")
+    if out.device != t.device or not out.is_contiguous() or out.dtype != t.dtype:
+        raise ValueError("out must be a contiguous tensor of t's dtype on t's device")
+    if out.numel() * out.element_size() != outer * row_bytes:
+        raise ValueError(f"out holds {out.numel() * out.element_size()} B, the slot's rows are "
+                         f"{outer * row_bytes} B")
+    rc = _lib.load().wkv7_slot_copy(out.data_ptr(), row_bytes, 0, 1, None,
+                                    t.data_ptr() + int(slot) * slot_stride, outer_stride, 0, 1,
+                                    None, outer, row_bytes, 1, _stream_ptr(t.device))
+    _lib.check(rc, "wkv7_slot_copy")
+
+
 def _slot_transfer(direction: int, t: torch.Tensor, slot: int, slot_dim: int,
-                   host: torch.Tensor) -> None:
+                   host: torch.Tensor, staging: torch.Tensor | None) -> None:
     _require_cuda(t, "slot tensor")
     outer, outer_stride, slot_stride, rows, row_bytes = slot_view(t, slot_dim)
     if not 0 <= int(slot) < rows:
@@ -350,29 +369,43 @@ def _slot_transfer(direction: int, t: torch.Tensor, slot: int, slot_dim: int,
                          f"the slot's rows are {outer * row_bytes} B")
     if not host.is_pinned():
         raise ValueError("host buffer must be pinned (pin_memory) for the DMA copy")
+    st_ptr, st_bytes = None, 0
+    if staging is not None:
+        if staging.device != t.device or not staging.is_contiguous():
+            raise ValueError("staging must be a contiguous tensor on the slot tensor's device")
+        st_bytes = staging.numel() * staging.element_size()
+        if st_bytes < outer * row_bytes:
+            raise ValueError(f"staging holds {st_bytes} B, the slot's rows are "
+                             f"{outer * row_bytes} B")
+        st_ptr = staging.data_ptr()
     rc = _lib.load().wkv7_slot_transfer(direction, host.data_ptr(), t.data_ptr(), outer_stride,
                                         slot_stride, rows, int(slot), outer, row_bytes,
-                                        _stream_ptr(t.device))
+                                        st_ptr, st_bytes, _stream_ptr(t.device))
     _lib.check(rc, "wkv7_slot_transfer")
 
 
 def slot_to_host(t: torch.Tensor, slot: int, slot_dim: int, host: torch.Tensor | None = None,
-                 ) -> torch.Tensor:
-    """Asynchronous DMA of one slot's rows of ``t`` (every outer block) into a
+                 staging: torch.Tensor | None = None) -> torch.Tensor:
+    """Asynchronous copy of one slot's rows of ``t`` (every outer block) into a
     dense pinned host tensor shaped like ``t.select(slot_dim, slot)``; the
-    caller synchronises before reading it."""
+    caller synchronises before reading it. With ``staging`` (a device tensor
+    of at least the slot's bytes) the rows are gathered on the device first
+    and cross the host link as one contiguous DMA; without it the DMA itself
+    is strided."""
     _require_cuda(t, "slot tensor")
     shape = t.shape[:slot_dim] + t.shape[slot_dim + 1:]
     if host is None:
         host = torch.empty(shape, dtype=t.dtype, pin_memory=True)
-    _slot_transfer(_lib.WKV7_TO_HOST, t, slot, slot_dim, host)
+    _slot_transfer(_lib.WKV7_TO_HOST, t, slot, slot_dim, host, staging)
     return host
 
 
-def slot_from_host(t: torch.Tensor, slot: int, slot_dim: int, host: torch.Tensor) -> None:
-    """Asynchronous DMA of a dense pinned host tensor (shaped like
-    ``t.select(slot_dim, slot)``) into one slot's rows of ``t``."""
-    _slot_transfer(_lib.WKV7_FROM_HOST, t, slot, slot_dim, host)
+def slot_from_host(t: torch.Tensor, slot: int, slot_dim: int, host: torch.Tensor,
+                   staging: torch.Tensor | None = None) -> None:
+    """Asynchronous copy of a dense pinned host tensor (shaped like
+    ``t.select(slot_dim, slot)``) into one slot's rows of ``t``; ``staging``
+    as for ``slot_to_host``."""
+    _slot_transfer(_lib.WKV7_FROM_HOST, t, slot, slot_dim, host, staging)
 
 
 def _overlaps(x: torch.Tensor, y: torch.Tensor) -> bool:

@@ -13,10 +13,12 @@ Interface, record fields, handle strings (``name@version``), file names, the
 index format and the model fingerprint follow the reference
 (wkvm/store.py:39-57, 63-86, 108-176, 195-243) so that stores written by
 either implementation load in the other. What changes is the HOT <-> WARM
-path: each family moves as one strided DMA copy between the slot rows and the
-pinned WARM tensor (``wkv7_slot_transfer``), where the reference copies a
-non-contiguous slot view with ``Tensor.copy_`` (wkvm/store.py:130-131,
-151-152, 230-233). Mutation rules act on WARM host tensors with the
+path, where the reference copies a non-contiguous slot view with
+``Tensor.copy_`` (wkvm/store.py:130-131, 151-152, 230-233): a save gathers
+both families' strided slot rows into a device staging buffer
+(``wkv7_slot_copy``) and then moves each to its pinned WARM tensor as one
+contiguous DMA; a load is one strided host-to-device DMA per family straight
+into the slot rows (``wkv7_slot_transfer``). Mutation rules act on WARM host tensors with the
 reference's arithmetic: ``decay`` scales ``wkv`` (wkvm/store.py:298-305),
 ``merge`` blends two records in fp32 (wkvm/store.py:260-268).
 
@@ -28,6 +30,7 @@ from __future__ import annotations
 
 import hashlib
 import json
+import math
 import os
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
@@ -85,6 +88,7 @@ class StateStore:
         self._meta: dict[str, StateRecord] = {}
         self._cold: set[str] = set()
         self._rules: dict[str, MutationRule] = {}
+        self._stage: torch.Tensor | None = None
         self.register_rule("decay", rule_decay)
         self.register_rule("merge", self._rule_merge)
         self._load_index()
@@ -113,18 +117,46 @@ class StateStore:
     def _family(self, name: str) -> torch.Tensor:
         return self.bank.wkv if name == "wkv" else self.bank.shift
 
+    def _staging(self) -> torch.Tensor:
+        """Device buffer holding one slot's rows of both families (12.2 MiB
+        at the 1.5B shape), allocated on first use: a save gathers the slot's
+        strided rows into it and each family crosses the host link as one
+        contiguous DMA."""
+        if self._stage is None:
+            nbytes = sum(-(-self._family(f).select(_SLOT_DIM[f], 0).numel()
+                           * self._family(f).element_size() // 256) * 256
+                         for f in ("wkv", "shift"))
+            self._stage = torch.empty(nbytes, dtype=torch.uint8, device=self.bank.device)
+        return self._stage
+
     def save(self, name: str, slots: dict[str, int], num_computed_tokens: int,
              token_ids: list[int], parent: str | None = None, rule: str | None = None,
              rule_params: dict | None = None) -> str:
-        """Snapshot a session's HOT slot rows into a new WARM record: one DMA
+        """Snapshot a session's HOT slot rows into a new WARM record: device
+        gathers of both families into the staging buffer, one contiguous DMA
         per family, then one synchronise (wkvm/store.py:108-137)."""
         record = StateRecord(name=name, version=self._next_version(name),
                              fingerprint=self.fingerprint,
                              num_computed_tokens=num_computed_tokens,
                              token_ids=tuple(token_ids), parent=parent, rule=rule,
                              rule_params=rule_params or {})
-        tensors = {fam: ops.slot_to_host(self._family(fam), slots[fam], _SLOT_DIM[fam])
-                   for fam in ("wkv", "shift")}
+        # Both families' rows are gathered into the staging buffer first, then
+        # moved to the host back to back: one kernel -> DMA hand-off per save.
+        staged = {}
+        offset = 0
+        staging = self._staging()
+        for fam in ("wkv", "shift"):
+            t = self._family(fam)
+            shape = t.shape[:_SLOT_DIM[fam]] + t.shape[_SLOT_DIM[fam] + 1:]
+            nbytes = math.prod(shape) * t.element_size()
+            staged[fam] = staging[offset:offset + nbytes].view(t.dtype).view(shape)
+            ops.slot_gather_dense(t, slots[fam], _SLOT_DIM[fam], staged[fam])
+            offset += -(-nbytes // 256) * 256
+        tensors = {}
+        for fam in ("wkv", "shift"):
+            tensors[fam] = torch.empty(staged[fam].shape, dtype=staged[fam].dtype,
+                                       pin_memory=True)
+            tensors[fam].copy_(staged[fam], non_blocking=True)
         torch.cuda.synchronize(self.bank.device)
         return self._add(record, tensors)
 
