@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 3
+#define WKV7_ABI_VERSION 4
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -188,6 +188,95 @@ int wkv7_slot_zero(void *base, int64_t outer_stride, int64_t slot_stride, int64_
 int wkv7_slot_transfer(int32_t direction, void *host, void *base, int64_t outer_stride,
                        int64_t slot_stride, int64_t rows, int32_t slot, int64_t outer,
                        int64_t row_bytes, void *staging, size_t staging_bytes, void *stream);
+
+/*
+ * Token shift of one state family, fused with the lerp mixes that consume it,
+ * for nseq ragged sequences (decode is nseq sequences of one token).
+ *
+ * For token t of sequence s (tokens cu_seqlens[s] .. cu_seqlens[s+1]-1):
+ *     prev     = x[t-1], or the slot's cached row shift_rows[slot_ids[s]]
+ *                for the sequence's first token
+ *     delta    = bf16(prev - x[t])
+ *     out[m,t] = bf16(fma(delta, mix[m], x[t]))    m = 0 .. n_mix-1
+ * and the sequence's last row of x becomes the slot's cached row (in place).
+ * A zero cached row is the zero shift-in at position 0 of a fresh sequence.
+ *
+ * Replaces the token-shift caches of the reference's RWKV-7 layers: the
+ * attention mixer's conv_state and the channel mixer's ffn_state, held per
+ * slot in bank.shift[:, 0] and bank.shift[:, 1] ([L, 2, S+1, D], model dtype,
+ * wkvm/runner/state.py:40-46; semantics wkvm/models/rwkv7.py:17-27), which
+ * the runner gathers into fla's Cache before each forward and scatters back
+ * after it (wkvm/runner/state.py:78-79, 92-97). The shift and the
+ * x + delta * mu mixes themselves run inside fla's RWKV7Attention /
+ * RWKV7FeedForward (external, not in the reference).
+ *
+ *   x            [total_tokens, D] bf16, the mixer's input
+ *   shift_rows   one layer and family of bank.shift: num_rows rows of D bf16,
+ *                row_stride elements apart (bank.shift[l, f] has row_stride D)
+ *   slot_ids     [nseq] int32 (device), distinct
+ *   cu_seqlens   [nseq + 1] int32 (device), as for wkv7_prefill_varlen
+ *   mix          [n_mix, D] bf16 (x_r, x_w, x_k, x_v, x_a, x_g for the
+ *                attention mixer; x_k for the channel mixer)
+ *   out          n_mix outputs of [total_tokens, D] bf16, out_stride elements
+ *                apart
+ * D, row_stride and out_stride must be multiples of 8 and x, shift_rows, mix
+ * and out 16-byte aligned (else WKV7_ERR_SHAPE).
+ */
+int wkv7_token_shift_mix(const uint16_t *x, int64_t total_tokens, int32_t D,
+                         uint16_t *shift_rows, int64_t num_rows, int64_t row_stride,
+                         const int32_t *slot_ids, const int32_t *cu_seqlens, int32_t nseq,
+                         const uint16_t *mix, int32_t n_mix, uint16_t *out,
+                         int64_t out_stride, void *stream);
+
+/*
+ * RWKV-7 time-mix projections -> the WKV7 op's inputs, per token and head
+ * (fp32 arithmetic, one bf16 rounding per output):
+ *     a     = sigmoid(a_lora)                 w_out = -exp(-0.5) * sigmoid(w_lora)
+ *     kk    = normalize(k * k_k) over the head (x / max(||x||_2, 1e-12))
+ *     k_out = k * (1 + (a - 1) * k_a)         a_out = -kk      b_out = kk * a
+ *     v_out = v + (v_first - v) * sigmoid(v_lora)   (v when v_lora is NULL)
+ * w_lora, a_lora and v_lora are the LoRA outputs including their biases
+ * (w0, a0, v0). w_out is the log-decay wkv7_decode_slots / _prefill_varlen
+ * take.
+ *
+ * Replaces the element-wise part of fla's RWKV7Attention between its
+ * projections and the wkv call (external; the reference calls it through the
+ * model forward, wkvm/runner/runner.py:80-88, wkvm/models/rwkv7.py:108-113).
+ *
+ *   k, v, w_lora, a_lora, v_lora, v_first, outputs   [total_tokens, H*64] bf16
+ *   k_k, k_a                                          [H*64] bf16
+ * v_lora and v_first are both NULL (first layer) or both set. Pointers must
+ * be 8-byte aligned (else WKV7_ERR_SHAPE).
+ */
+int wkv7_time_mix_inputs(int64_t total_tokens, int32_t H, const uint16_t *k,
+                         const uint16_t *v, const uint16_t *w_lora, const uint16_t *a_lora,
+                         const uint16_t *v_lora, const uint16_t *v_first,
+                         const uint16_t *k_k, const uint16_t *k_a, uint16_t *w_out,
+                         uint16_t *k_out, uint16_t *v_out, uint16_t *a_out, uint16_t *b_out,
+                         void *stream);
+
+/*
+ * RWKV-7 time-mix output stage, per token and head (fp32 arithmetic, one
+ * bf16 rounding per output):
+ *     n   = (y - mean(y)) / sqrt(var(y) + eps) * ln_w + ln_b   (biased var)
+ *     out = (n + (sum_c r k r_k) * v) * g
+ * i.e. the per-head GroupNorm of the WKV output, the bonus term and the gate;
+ * `out` is the input of the output projection.
+ *
+ * Replaces fla's g_norm, bonus and gate in RWKV7Attention (external; reached
+ * through the model forward, wkvm/runner/runner.py:80-88).
+ *
+ *   y            [total_tokens, H, 64], dtype per y_dtype (the WKV output)
+ *   r, k, v, g   [total_tokens, H*64] bf16 (k and v as fed to the WKV op)
+ *   r_k          [H*64] bf16;  ln_w, ln_b [H*64] bf16 (GroupNorm affine)
+ *   out          [total_tokens, H*64] bf16
+ * Pointers must be 8-byte aligned, y 16-byte aligned when fp32 (else
+ * WKV7_ERR_SHAPE).
+ */
+int wkv7_time_mix_output(int64_t total_tokens, int32_t H, const void *y, int32_t y_dtype,
+                         const uint16_t *r, const uint16_t *k, const uint16_t *v,
+                         const uint16_t *g, const uint16_t *r_k, const uint16_t *ln_w,
+                         const uint16_t *ln_b, float eps, uint16_t *out, void *stream);
 
 #ifdef __cplusplus
 }

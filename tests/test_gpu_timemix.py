@@ -1,0 +1,223 @@
+"""Time-mix stages on the GPU (HIP kernels through the C ABI) against the CPU
+oracle (oracle/timemix.py), plus the composed RWKV-7 time-mix block.
+
+Bars: ``token_shift_mix`` is bit-exact (outputs and the slot rows it writes;
+rows outside the batch, pad row 0 included, untouched). ``time_mix_inputs``
+and ``time_mix_output`` compute in fp32 with hardware exp / reciprocal, so a
+bf16 output may land one bf16 ulp from the float64 value rounded to bf16:
+inputs are held to <= 1 ulp (absolute 2^-8 |ref| at the rounding edge),
+except the v lerp, which can cancel and is held to 2^-8 of its summands'
+magnitude; the output to 2^-7 of its summands' magnitude (the GroupNorm and
+the bonus term can cancel).
+
+The composed block must give the same shift rows (bit-exact) whether a prompt
+runs as one prefill, as two chunks through the slot, or token by token as
+decode steps, and the same wkv state and outputs to 1e-2. The projections
+are vendor-BLAS GEMMs whose accumulation order depends on the row count, so
+their bf16 outputs (the WKV inputs) differ by an ulp here and there between
+those runs (state differences ~5e-4 measured); a broken hand-off through the
+slot (a stale shift row, a reset or double-applied state) differs by O(0.1)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import timemix as TM
+from tests import util as U
+from wkvm_amd import ops
+from wkvm_amd.layout import RWKV7StateLayout
+from wkvm_amd.state import RWKV7StateBank
+from wkvm_amd.timemix import RWKV7TimeMix, TokenBatch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(shape, dev, seed, scale=1.0):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("D,rows,slots,cu,M", [
+    (768, 17, [3, 9, 1, 16], None, 6),                   # decode, 0.1B width
+    (2048, 9, [2, 7, 4, 5, 8], [0, 5, 5, 40, 41, 57], 6),  # ragged prefill, an empty sequence
+    (2048, 9, [6], [0, 1], 1),                           # one token, channel-mix family (M = 1)
+    (4096, 5, [1, 3], [0, 130, 131], 6),                 # 7B width, D = 2 block passes
+])
+def test_token_shift_mix_bit_exact(dev, D, rows, slots, cu, M):
+    T = len(slots) if cu is None else cu[-1]
+    x = _bf((T, D), dev, 1)
+    shift = _bf((3, 2, rows, D), dev, 2)  # [L, 2, S+1, D] like bank.shift
+    mix = (torch.rand((M, D), generator=torch.Generator(device=dev).manual_seed(3), device=dev)
+           ).to(torch.bfloat16)
+    fam = 1 if M == 1 else 0
+    before = shift.clone()
+    out = ops.token_shift_mix(x, shift[1, fam], slots, mix, cu)
+    torch.cuda.synchronize()
+    ref_out, ref_shift = TM.token_shift_mix(U.bits(x), U.bits(before[1, fam]), slots,
+                                            cu if cu is not None else range(T + 1), U.bits(mix))
+    assert np.array_equal(U.bits(out), ref_out)
+    assert np.array_equal(U.bits(shift[1, fam]), ref_shift)
+    # other layers and the other family are untouched
+    keep = shift.clone()
+    keep[1, fam] = before[1, fam]
+    assert torch.equal(keep, before)
+
+
+def test_token_shift_mix_full_decode_shape(dev):
+    """Config-1 shape: 256 slots of a 512-slot pool, D = 2048, six mixes."""
+    D, rows = 2048, 513
+    gen = torch.Generator().manual_seed(11)
+    slots = (torch.randperm(512, generator=gen)[:256] + 1).tolist()
+    x = _bf((256, D), dev, 4)
+    shift = _bf((rows, D), dev, 5)
+    mix = _bf((6, D), dev, 6, 0.5)
+    before = U.bits(shift)
+    out = ops.token_shift_mix(x, shift, slots, mix)
+    torch.cuda.synchronize()
+    ref_out, ref_shift = TM.token_shift_mix(U.bits(x), before, slots, range(257), U.bits(mix))
+    assert np.array_equal(U.bits(out), ref_out)
+    assert np.array_equal(U.bits(shift), ref_shift)
+
+
+def _input_args(T, H, dev, seed, with_v=True):
+    D = H * 64
+    names = ["k", "v", "w_lora", "a_lora"]
+    a = {n: _bf((T, D), dev, seed + i) for i, n in enumerate(names)}
+    a["k_k"] = (0.5 + torch.rand(D, generator=torch.Generator(device=dev).manual_seed(seed + 9),
+                                 device=dev)).to(torch.bfloat16)
+    a["k_a"] = torch.rand(D, generator=torch.Generator(device=dev).manual_seed(seed + 10),
+                          device=dev).to(torch.bfloat16)
+    if with_v:
+        a["v_lora"] = _bf((T, D), dev, seed + 11)
+        a["v_first"] = _bf((T, D), dev, seed + 12)
+    return a
+
+
+def _ulp_ok(got: torch.Tensor, ref: np.ndarray) -> None:
+    ulps = U.bf16_ulp_distance(U.bits(got), ref)
+    edge = np.abs(U.f64(got) - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30
+    assert np.all((ulps <= 1) | edge), f"max {ulps.max()} ulps"
+
+
+@pytest.mark.parametrize("T,H,with_v", [(7, 12, False), (256, 32, True), (3000, 32, True)])
+def test_time_mix_inputs_match_oracle(dev, T, H, with_v):
+    a = _input_args(T, H, dev, 20, with_v)
+    outs = ops.time_mix_inputs(H, **a)
+    torch.cuda.synchronize()
+    f = {n: U.f64(t) for n, t in a.items()}
+    ref = TM.time_mix_inputs(H, **f)
+    for name, got in zip("wkvab", outs):
+        if name == "v" and with_v:
+            # the lerp can cancel: bound by its summands' magnitude
+            s = 1.0 / (1.0 + np.exp(-f["v_lora"]))
+            scale = np.abs(f["v"]) + np.abs(f["v_first"] - f["v"]) * s
+            assert np.all(np.abs(U.f64(got) - ref["v"]) <= 2.0 ** -8 * scale + 1e-30)
+        else:
+            _ulp_ok(got, ref[name])
+
+
+@pytest.mark.parametrize("T,H,y_dtype", [(5, 12, torch.float32), (256, 32, torch.bfloat16),
+                                         (2000, 32, torch.float32)])
+def test_time_mix_output_matches_oracle(dev, T, H, y_dtype):
+    D = H * 64
+    y = (torch.randn((T, H, 64), generator=torch.Generator(device=dev).manual_seed(30),
+                     device=dev) * 2 + 0.3).to(y_dtype)
+    r, k, v, g = (_bf((T, D), dev, 31 + i) for i in range(4))
+    r_k = _bf((D,), dev, 40, 0.3)
+    ln_w = (0.8 + 0.4 * torch.rand(D, generator=torch.Generator(device=dev).manual_seed(41),
+                                   device=dev)).to(torch.bfloat16)
+    ln_b = _bf((D,), dev, 42, 0.1)
+    eps = 64e-5
+    out = ops.time_mix_output(H, y, r, k, v, g, r_k, ln_w, ln_b, eps)
+    torch.cuda.synchronize()
+    ref, scale = TM.time_mix_output(H, U.f64(y), *(U.f64(t) for t in (r, k, v, g, r_k, ln_w,
+                                                                       ln_b)), eps)
+    err = np.abs(U.f64(out) - ref)
+    assert np.all(err <= 2.0 ** -7 * scale + 1e-30), f"max err/scale {np.max(err / scale):.2e}"
+
+
+# -- the composed block ------------------------------------------------------------------
+
+def _block(dev, shape="0.1B", slots=6):
+    layout = RWKV7StateLayout.for_shape(shape)
+    bank = RWKV7StateBank(layout, slots, device=dev)
+    bank.wkv.normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(50))
+    bank.shift.copy_(_bf(bank.shift.shape, dev, 51))
+    layers = [RWKV7TimeMix.random(layout, l, dev, seed=3) for l in range(2)]
+    return layout, bank, layers
+
+
+def _run(bank, layers, x, slots, cu):
+    batch = TokenBatch.plan(bank, slots, cu)
+    v_first = None
+    outs = []
+    for layer in layers:
+        o, v_first = layer.forward(bank, x, batch, v_first)
+        outs.append(o)
+    return outs
+
+
+def test_block_prefill_equals_chunks_and_decode(dev):
+    layout, bank0, layers = _block(dev)
+    T, slot = 40, 4
+    x = _bf((T, layout.hidden_size), dev, 60)
+    banks = []
+    for _ in range(3):
+        b = RWKV7StateBank(layout, bank0.num_slots, device=dev)
+        b.wkv.copy_(bank0.wkv)
+        b.shift.copy_(bank0.shift)
+        banks.append(b)
+    # one prefill
+    full = _run(banks[0], layers, x, [slot], [0, T])
+    # two chunks threaded through the slot
+    c1 = _run(banks[1], layers, x[:17], [slot], [0, 17])
+    c2 = _run(banks[1], layers, x[17:], [slot], [0, T - 17])
+    # token by token as decode steps
+    steps = [_run(banks[2], layers, x[t:t + 1], [slot], None) for t in range(T)]
+    torch.cuda.synchronize()
+    for name, b in zip(("chunked", "decode"), banks[1:]):
+        assert torch.equal(b.shift, banks[0].shift), "shift rows differ"
+        err = U.normwise_max(U.f64(b.wkv[:, slot]), U.f64(banks[0].wkv[:, slot]))
+        print(f"{name}: wkv state normwise difference {err:.2e}")
+        assert err <= 1e-2, f"{name}: wkv state differs by {err:.2e}"
+    others = [i for i in range(bank0.num_slots + 1) if i != slot]
+    assert torch.equal(banks[0].wkv[:, others], bank0.wkv[:, others])
+    assert torch.equal(banks[0].shift[:, :, others], bank0.shift[:, :, others])
+    for l in range(len(layers)):
+        ref = U.f64(full[l])
+        chunked = np.concatenate([U.f64(c1[l]), U.f64(c2[l])])
+        dec = np.concatenate([U.f64(s[l]) for s in steps])
+        print(f"layer {l}: output rel-L2 chunked {U.rel_l2(chunked, ref):.2e}, "
+              f"decode {U.rel_l2(dec, ref):.2e}")
+        assert U.rel_l2(chunked, ref) <= 1e-2, f"layer {l}: chunked {U.rel_l2(chunked, ref):.2e}"
+        assert U.rel_l2(dec, ref) <= 1e-2, f"layer {l}: decode {U.rel_l2(dec, ref):.2e}"
+
+
+def test_block_ragged_batch_equals_separate_requests(dev):
+    """One ragged launch over three requests (one of them a single token)
+    equals running each request alone (wkvm/engine.py:142-170 runs them one by
+    one)."""
+    layout, bank0, layers = _block(dev)
+    lens, slots = [9, 1, 22], [2, 5, 3]
+    cu = [0, 9, 10, 32]
+    x = _bf((32, layout.hidden_size), dev, 70)
+    together = RWKV7StateBank(layout, bank0.num_slots, device=dev)
+    together.wkv.copy_(bank0.wkv)
+    together.shift.copy_(bank0.shift)
+    outs = _run(together, layers, x, slots, cu)
+    alone = RWKV7StateBank(layout, bank0.num_slots, device=dev)
+    alone.wkv.copy_(bank0.wkv)
+    alone.shift.copy_(bank0.shift)
+    parts = [_run(alone, layers, x[cu[i]:cu[i + 1]], [slots[i]], [0, lens[i]]) for i in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(together.shift, alone.shift)
+    err = U.normwise_max(U.f64(together.wkv), U.f64(alone.wkv))
+    print(f"ragged vs separate: wkv state normwise difference {err:.2e}")
+    assert err <= 1e-2
+    for l in range(len(layers)):
+        sep = np.concatenate([U.f64(p[l]) for p in parts])
+        assert U.rel_l2(U.f64(outs[l]), sep) <= 1e-2

@@ -46,6 +46,12 @@ SIGNATURES = {
     "wkv7_slot_zero": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
     "wkv7_slot_transfer": (ctypes.c_int, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _i64, _i64,
                                          _vp, _sz, _vp]),
+    "wkv7_token_shift_mix": (ctypes.c_int, [
+        _vp, _i64, _i32, _vp, _i64, _i64, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _vp]),
+    "wkv7_time_mix_inputs": (ctypes.c_int, [
+        _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "wkv7_time_mix_output": (ctypes.c_int, [
+        _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,305 @@
+// RWKV-7 time-mix element-wise stages around the WKV7 op, over the slot pool.
+//
+//  * token_shift_mix: the token shift of one state family (bank.shift[l, f],
+//    [num_rows, D] bf16, row 0 = pad slot) fused with the lerp mixes that
+//    consume it. Token t of sequence s sees prev = x[t-1], or the slot's
+//    cached row for the sequence's first token; the sequence's last row of x
+//    becomes the slot's cache (in place). Outputs
+//        out[m][t] = bf16(x[t] + bf16(prev - x[t]) * mix[m])   (one fp32 fma)
+//  * time_mix_inputs: projection outputs -> the WKV op's inputs (log-decay w,
+//    k, v, a = -kk, b = kk * a) with the per-head L2 normalisation of
+//    kk = k * k_k.
+//  * time_mix_output: per-head GroupNorm of the WKV output, the bonus term
+//    (sum_c r k r_k) v and the output gate.
+//
+// All three are HBM-streaming kernels: 16-byte vector loads and stores of
+// bf16 rows, fp32 arithmetic, one bf16 rounding per output element. A head
+// (64 channels) is 16 lanes x 4 channels, so per-head sums are reductions
+// inside one 16-lane DPP row.
+#include "wkv7_common.h"
+
+namespace wkv7 {
+namespace {
+
+constexpr int kMixThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+// RWKV-7 log-decay scale: w = -exp(-0.5) * sigmoid(.) (decay in (0.545, 1))
+constexpr float kDecayScale = 0.6065306597126334f;
+
+struct Bf8 {
+  uint32_t p[4];  // 8 bf16, element 2i in the low half of p[i]
+};
+
+__device__ __forceinline__ Bf8 ld8(const uint16_t* p) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  return Bf8{{v.x, v.y, v.z, v.w}};
+}
+__device__ __forceinline__ void st8(uint16_t* p, const Bf8& v) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(v.p[0], v.p[1], v.p[2], v.p[3]);
+}
+__device__ __forceinline__ float el(const Bf8& v, int e) {
+  return (e & 1) ? bf16_hi(v.p[e >> 1]) : bf16_lo(v.p[e >> 1]);
+}
+
+// Sequence of token t: the largest s with cu[s] <= t (empty sequences have
+// cu[s] == cu[s+1] and are skipped by taking the largest such s).
+__device__ __forceinline__ int seq_of(const int32_t* cu, int nseq, int64_t t) {
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (int64_t(cu[mid]) <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kMixThreads) void token_shift_mix_kernel(
+    const uint16_t* __restrict__ x, int64_t T, int D, uint16_t* __restrict__ shift,
+    int64_t num_rows, int64_t row_stride, const int32_t* __restrict__ slot_ids,
+    const int32_t* __restrict__ cu, int nseq, const uint16_t* __restrict__ mix, int n_mix,
+    uint16_t* __restrict__ out, int64_t out_stride) {
+  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
+    const int s = seq_of(cu, nseq, t);
+    const int64_t beg = max(int64_t(cu[s]), int64_t(0)), end = min(int64_t(cu[s + 1]), T);
+    if (t < beg || t >= end) continue;  // tokens outside every sequence (uniform)
+    const bool first = t == beg;
+    const int64_t slot = first ? int64_t(slot_ids[s]) : -1;
+    const bool cached = slot >= 0 && slot < num_rows;
+    for (int c = 8 * threadIdx.x; c < D; c += 8 * kMixThreads) {
+      const Bf8 xv = ld8(x + t * D + c);
+      Bf8 pv{{0u, 0u, 0u, 0u}};
+      if (!first) {
+        pv = ld8(x + (t - 1) * D + c);
+      } else if (cached) {
+        uint16_t* row = shift + slot * row_stride + c;
+        pv = ld8(row);
+        st8(row, ld8(x + (end - 1) * D + c));  // the sequence's last row becomes the cache
+      }
+      float xf[8], df[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xf[e] = el(xv, e);
+        // prev - x of two bf16 values is exact in fp32; the shift's output is bf16
+        df[e] = bf16_lo(pack_bf16(el(pv, e) - xf[e], 0.f));
+      }
+      for (int m = 0; m < n_mix; ++m) {
+        const Bf8 mu = ld8(mix + int64_t(m) * D + c);
+        Bf8 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o.p[i] = pack_bf16(fmaf(df[2 * i], el(mu, 2 * i), xf[2 * i]),
+                             fmaf(df[2 * i + 1], el(mu, 2 * i + 1), xf[2 * i + 1]));
+        st8(out + int64_t(m) * out_stride + t * D + c, o);
+      }
+    }
+  }
+}
+
+// Four bf16 of a 16-lane head slice (8-byte loads).
+struct Bf4 {
+  uint32_t p[2];
+};
+__device__ __forceinline__ Bf4 ld4(const uint16_t* p) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  return Bf4{{v.x, v.y}};
+}
+__device__ __forceinline__ void st4(uint16_t* p, float a, float b, float c, float d) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16(a, b), pack_bf16(c, d));
+}
+__device__ __forceinline__ float el(const Bf4& v, int e) {
+  return (e & 1) ? bf16_hi(v.p[e >> 1]) : bf16_lo(v.p[e >> 1]);
+}
+
+// Sum over the 16 lanes of a DPP row (butterfly: every lane gets the total).
+__device__ __forceinline__ float row_sum16(float x) {
+  x += __shfl_xor(x, 1, 16);
+  x += __shfl_xor(x, 2, 16);
+  x += __shfl_xor(x, 4, 16);
+  x += __shfl_xor(x, 8, 16);
+  return x;
+}
+
+__device__ __forceinline__ float sigmoidf(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+struct MixIn {
+  const uint16_t *k, *v, *w_lora, *a_lora, *v_lora, *v_first, *k_k, *k_a;
+};
+struct MixOut {
+  uint16_t *w, *k, *v, *a, *b;
+};
+
+// One (token, head) per 16 lanes, 4 channels per lane.
+__global__ __launch_bounds__(kMixThreads) void time_mix_inputs_kernel(int64_t units, int H,
+                                                                       MixIn in, MixOut out) {
+  const int64_t unit = (int64_t(blockIdx.x) * kMixThreads + threadIdx.x) >> 4;
+  if (unit >= units) return;  // whole 16-lane groups leave together
+  const int sub = threadIdx.x & 15;
+  const int64_t h = unit % H;
+  const int64_t o = unit * kHead + 4 * sub;  // element offset: token row, head, channels
+  const int pc = int(h * kHead + 4 * sub);   // parameter offset (channel within D)
+  const Bf4 k = ld4(in.k + o), v = ld4(in.v + o), wl = ld4(in.w_lora + o), al = ld4(in.a_lora + o);
+  const Bf4 kk_s = ld4(in.k_k + pc), ka = ld4(in.k_a + pc);
+  float kk[4], a[4], ssq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    kk[e] = el(k, e) * el(kk_s, e);
+    ssq = fmaf(kk[e], kk[e], ssq);
+    a[e] = sigmoidf(el(al, e));
+  }
+  ssq = row_sum16(ssq);
+  // x / max(||x||, 1e-12), the F.normalize convention
+  const float inv = 1.f / fmaxf(sqrtf(ssq), 1e-12f);
+  float wv[4], kv[4], vv[4], av[4], bv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float n = kk[e] * inv;
+    wv[e] = -kDecayScale * sigmoidf(el(wl, e));
+    kv[e] = el(k, e) * fmaf(a[e] - 1.f, el(ka, e), 1.f);
+    av[e] = -n;
+    bv[e] = n * a[e];
+    vv[e] = el(v, e);
+  }
+  if (in.v_lora) {  // uniform: lerp(v, v_first, sigmoid(v_lora)) for layers > 0
+    const Bf4 vl = ld4(in.v_lora + o), vf = ld4(in.v_first + o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vv[e] = fmaf(el(vf, e) - vv[e], sigmoidf(el(vl, e)), vv[e]);
+  }
+  st4(out.w + o, wv[0], wv[1], wv[2], wv[3]);
+  st4(out.k + o, kv[0], kv[1], kv[2], kv[3]);
+  st4(out.v + o, vv[0], vv[1], vv[2], vv[3]);
+  st4(out.a + o, av[0], av[1], av[2], av[3]);
+  st4(out.b + o, bv[0], bv[1], bv[2], bv[3]);
+}
+
+struct OutIn {
+  const void* y;
+  const uint16_t *r, *k, *v, *g, *r_k, *ln_w, *ln_b;
+};
+
+template <bool kF32Y>
+__global__ __launch_bounds__(kMixThreads) void time_mix_output_kernel(int64_t units, int H,
+                                                                       OutIn in, float eps,
+                                                                       uint16_t* __restrict__ out) {
+  const int64_t unit = (int64_t(blockIdx.x) * kMixThreads + threadIdx.x) >> 4;
+  if (unit >= units) return;
+  const int sub = threadIdx.x & 15;
+  const int64_t h = unit % H;
+  const int64_t o = unit * kHead + 4 * sub;
+  const int pc = int(h * kHead + 4 * sub);
+  float y[4];
+  if (kF32Y) {
+    const float4 yv = *reinterpret_cast<const float4*>(static_cast<const float*>(in.y) + o);
+    y[0] = yv.x; y[1] = yv.y; y[2] = yv.z; y[3] = yv.w;
+  } else {
+    const Bf4 yv = ld4(static_cast<const uint16_t*>(in.y) + o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = el(yv, e);
+  }
+  const Bf4 r = ld4(in.r + o), k = ld4(in.k + o), v = ld4(in.v + o), g = ld4(in.g + o);
+  const Bf4 rk = ld4(in.r_k + pc), lw = ld4(in.ln_w + pc), lb = ld4(in.ln_b + pc);
+  float sum = 0.f, bonus = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sum += y[e];
+    bonus = fmaf(el(r, e) * el(k, e), el(rk, e), bonus);
+  }
+  const float mean = row_sum16(sum) * (1.f / kHead);
+  bonus = row_sum16(bonus);
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] -= mean;
+    sq = fmaf(y[e], y[e], sq);
+  }
+  const float rstd = 1.f / sqrtf(row_sum16(sq) * (1.f / kHead) + eps);  // biased variance
+  float ov[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    ov[e] = (fmaf(y[e] * rstd, el(lw, e), el(lb, e)) + bonus * el(v, e)) * el(g, e);
+  st4(out + o, ov[0], ov[1], ov[2], ov[3]);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+unsigned unit_grid(int64_t units) {
+  const int64_t per_block = kMixThreads / 16;
+  return static_cast<unsigned>((units + per_block - 1) / per_block);
+}
+
+}  // namespace
+}  // namespace wkv7
+
+using namespace wkv7;
+
+extern "C" int wkv7_token_shift_mix(const uint16_t* x, int64_t total_tokens, int32_t D,
+                                    uint16_t* shift_rows, int64_t num_rows, int64_t row_stride,
+                                    const int32_t* slot_ids, const int32_t* cu_seqlens,
+                                    int32_t nseq, const uint16_t* mix, int32_t n_mix,
+                                    uint16_t* out, int64_t out_stride, void* stream) {
+  if (total_tokens < 0 || D < 1 || nseq < 0 || n_mix < 0 || num_rows < 1 || row_stride < D)
+    return WKV7_ERR_ARG;
+  if (total_tokens == 0 || nseq == 0) return WKV7_OK;
+  if (!x || !shift_rows || !slot_ids || !cu_seqlens || (n_mix > 0 && (!mix || !out)))
+    return WKV7_ERR_ARG;
+  if (n_mix > 1 && out_stride < total_tokens * int64_t(D)) return WKV7_ERR_ARG;
+  if ((D & 7) || (row_stride & 7) || (out_stride & 7) || !aligned16(x) || !aligned16(shift_rows) ||
+      (n_mix > 0 && (!aligned16(mix) || !aligned16(out))))
+    return WKV7_ERR_SHAPE;
+  const int64_t cap = int64_t(1) << 20;
+  const unsigned grid = static_cast<unsigned>(total_tokens < cap ? total_tokens : cap);
+  token_shift_mix_kernel<<<grid, kMixThreads, 0, as_stream(stream)>>>(
+      x, total_tokens, D, shift_rows, num_rows, row_stride, slot_ids, cu_seqlens, nseq, mix, n_mix,
+      out, out_stride);
+  return launch_status();
+}
+
+extern "C" int wkv7_time_mix_inputs(int64_t total_tokens, int32_t H, const uint16_t* k,
+                                    const uint16_t* v, const uint16_t* w_lora,
+                                    const uint16_t* a_lora, const uint16_t* v_lora,
+                                    const uint16_t* v_first, const uint16_t* k_k,
+                                    const uint16_t* k_a, uint16_t* w_out, uint16_t* k_out,
+                                    uint16_t* v_out, uint16_t* a_out, uint16_t* b_out,
+                                    void* stream) {
+  if (total_tokens < 0 || H < 1) return WKV7_ERR_ARG;
+  if (total_tokens == 0) return WKV7_OK;
+  if (!k || !v || !w_lora || !a_lora || !k_k || !k_a || !w_out || !k_out || !v_out || !a_out ||
+      !b_out || (v_lora != nullptr) != (v_first != nullptr))
+    return WKV7_ERR_ARG;
+  const void* ptrs[] = {k, v, w_lora, a_lora, k_k, k_a, w_out, k_out, v_out, a_out, b_out};
+  for (const void* p : ptrs)
+    if (!aligned8(p)) return WKV7_ERR_SHAPE;
+  if (v_lora && (!aligned8(v_lora) || !aligned8(v_first))) return WKV7_ERR_SHAPE;
+  const int64_t units = total_tokens * H;
+  if (units > int64_t(0x7fffffff) / 16) return WKV7_ERR_ARG;
+  time_mix_inputs_kernel<<<unit_grid(units), kMixThreads, 0, as_stream(stream)>>>(
+      units, H, MixIn{k, v, w_lora, a_lora, v_lora, v_first, k_k, k_a},
+      MixOut{w_out, k_out, v_out, a_out, b_out});
+  return launch_status();
+}
+
+extern "C" int wkv7_time_mix_output(int64_t total_tokens, int32_t H, const void* y,
+                                    int32_t y_dtype, const uint16_t* r, const uint16_t* k,
+                                    const uint16_t* v, const uint16_t* g, const uint16_t* r_k,
+                                    const uint16_t* ln_w, const uint16_t* ln_b, float eps,
+                                    uint16_t* out, void* stream) {
+  if (total_tokens < 0 || H < 1 || !(eps >= 0.f)) return WKV7_ERR_ARG;
+  if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
+  if (total_tokens == 0) return WKV7_OK;
+  if (!y || !r || !k || !v || !g || !r_k || !ln_w || !ln_b || !out) return WKV7_ERR_ARG;
+  const void* ptrs[] = {r, k, v, g, r_k, ln_w, ln_b, out};
+  for (const void* p : ptrs)
+    if (!aligned8(p)) return WKV7_ERR_SHAPE;
+  if (y_dtype == WKV7_Y_F32 ? !aligned16(y) : !aligned8(y)) return WKV7_ERR_SHAPE;
+  const int64_t units = total_tokens * H;
+  if (units > int64_t(0x7fffffff) / 16) return WKV7_ERR_ARG;
+  const OutIn in{y, r, k, v, g, r_k, ln_w, ln_b};
+  if (y_dtype == WKV7_Y_F32)
+    time_mix_output_kernel<true><<<unit_grid(units), kMixThreads, 0, as_stream(stream)>>>(
+        units, H, in, eps, out);
+  else
+    time_mix_output_kernel<false><<<unit_grid(units), kMixThreads, 0, as_stream(stream)>>>(
+        units, H, in, eps, out);
+  return launch_status();
+}

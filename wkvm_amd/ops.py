@@ -8,6 +8,9 @@ Two layers of API:
 
 * slot-indexed ops (the hot path): ``wkv7_decode_slots``,
   ``wkv7_prefill_varlen``, ``slot_copy``, ``slot_zero``;
+* the time-mix stages either side of the WKV op: ``token_shift_mix`` (the
+  slot-indexed token shift of a ``bank.shift`` family fused with its lerp
+  mixes), ``time_mix_inputs`` and ``time_mix_output``;
 * the fla wkv-op signatures the reference's model layer calls
   (``fused_recurrent_rwkv7`` for T < 64 and ``chunk_rwkv7`` otherwise,
   dispatched at wkvm/models/rwkv7.py:108-111), implemented by treating the
@@ -423,6 +426,161 @@ def slot_zero(t: torch.Tensor, ids, slot_dim: int) -> None:
     rc = _lib.load().wkv7_slot_zero(t.data_ptr(), os_, ss, rows, ids_t.data_ptr(), outer, rb, n,
                                     _stream_ptr(t.device))
     _lib.check(rc, "wkv7_slot_zero")
+
+
+# -- time-mix stages around the WKV op ------------------------------------------------
+
+def _bf16_2d(t: torch.Tensor, what: str, shape: tuple[int, ...] | None = None) -> torch.Tensor:
+    _require_cuda(t, what)
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{what} must be bfloat16, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{what} must be {tuple(shape)}, got {tuple(t.shape)}")
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def seq_plan(slot_ids, cu_seqlens, rows: int, T: int,
+             device: torch.device) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """Device ``(slot_ids, cu_seqlens, nseq)`` for a ragged token batch.
+    ``cu_seqlens=None`` is a decode batch (one token per slot). Host inputs
+    are validated and uploaded in one copy; device tensors pass through."""
+    if isinstance(slot_ids, torch.Tensor) and slot_ids.is_cuda:
+        ids = device_ids(slot_ids, rows, device, "slot_ids")
+        nseq = int(ids.shape[0])
+        if cu_seqlens is None:
+            if nseq != T:
+                raise ValueError(f"{nseq} slots for {T} decode tokens")
+            cu = torch.arange(nseq + 1, dtype=torch.int32, device=device)
+        elif isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.is_cuda:
+            if cu_seqlens.dtype != torch.int32 or cu_seqlens.shape != (nseq + 1,):
+                raise ValueError("device cu_seqlens must be int32 [nseq + 1]")
+            cu = cu_seqlens
+        else:
+            lst = _host_cu(cu_seqlens, T)
+            if len(lst) != nseq + 1:
+                raise ValueError(f"cu_seqlens has {len(lst)} entries for {nseq} sequences")
+            cu = torch.tensor(lst, dtype=torch.int32, device=device)
+        return ids, cu, nseq
+    lst = host_ids(slot_ids, rows, "slot_ids", distinct=True)
+    nseq = len(lst)
+    if cu_seqlens is None:
+        if nseq != T:
+            raise ValueError(f"{nseq} slots for {T} decode tokens")
+        cu_l = list(range(nseq + 1))
+    else:
+        cu_l = _host_cu(cu_seqlens, T)
+        if len(cu_l) != nseq + 1:
+            raise ValueError(f"cu_seqlens has {len(cu_l)} entries for {nseq} sequences")
+    both = torch.tensor(lst + cu_l, dtype=torch.int32, device=device)
+    return both[:nseq], both[nseq:], nseq
+
+
+def token_shift_mix(x: torch.Tensor, shift_rows: torch.Tensor, slot_ids, mix: torch.Tensor,
+                    cu_seqlens=None, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Token shift of one state family fused with its lerp mixes.
+
+    ``x [T, D]`` bf16 (the mixer's input), ``shift_rows [rows, D]`` bf16 (one
+    layer and family of ``bank.shift``, e.g. ``bank.shift[l, 0]``), ``mix
+    [M, D]`` bf16. ``cu_seqlens=None`` means one token per slot (decode).
+    Returns ``out [M, T, D]``: ``bf16(x + bf16(prev - x) * mix[m])`` with
+    prev the previous token, or the slot's row for a sequence's first token;
+    each sequence's last row of ``x`` becomes its slot's row (in place)."""
+    _require_cuda(shift_rows, "shift_rows")
+    if shift_rows.dtype != torch.bfloat16 or shift_rows.dim() != 2 or shift_rows.stride(1) != 1:
+        raise ValueError("shift_rows must be a bf16 [rows, D] view with unit channel stride")
+    rows, D = int(shift_rows.shape[0]), int(shift_rows.shape[1])
+    if x.dim() != 2 or int(x.shape[1]) != D:
+        raise ValueError(f"x must be [T, {D}], got {tuple(x.shape)}")
+    x = _bf16_2d(x, "x")
+    T = int(x.shape[0])
+    if mix.dim() != 2 or int(mix.shape[1]) != D:
+        raise ValueError(f"mix must be [M, {D}], got {tuple(mix.shape)}")
+    mix = _bf16_2d(mix, "mix")
+    M = int(mix.shape[0])
+    dev = x.device
+    if shift_rows.device != dev or mix.device != dev:
+        raise ValueError("x, shift_rows and mix must share a device")
+    if D % 8 or shift_rows.stride(0) % 8 or shift_rows.data_ptr() % 16:
+        raise ValueError("D and the shift row stride must be multiples of 8 (16-byte rows)")
+    ids, cu, nseq = seq_plan(slot_ids, cu_seqlens, rows, T, dev)
+    y = _out(out, (M, T, D), torch.bfloat16, dev, "out")
+    if y.dtype != torch.bfloat16 or y.data_ptr() % 16:
+        raise ValueError("out must be a 16-byte aligned bf16 tensor")
+    if T == 0 or nseq == 0:
+        return y
+    rc = _lib.load().wkv7_token_shift_mix(x.data_ptr(), T, D, shift_rows.data_ptr(), rows,
+                                          int(shift_rows.stride(0)), ids.data_ptr(),
+                                          cu.data_ptr(), nseq, mix.data_ptr(), M, y.data_ptr(),
+                                          T * D, _stream_ptr(dev))
+    _lib.check(rc, "wkv7_token_shift_mix")
+    return y
+
+
+def time_mix_inputs(H: int, k, v, w_lora, a_lora, k_k, k_a, v_lora=None, v_first=None):
+    """WKV op inputs from the time-mix projections, all ``[T, H*64]`` bf16
+    (``k_k``, ``k_a`` ``[H*64]``). ``v_lora``/``v_first`` are given together
+    (layers after the first). Returns ``(w, k, v, a, b)`` ``[T, H*64]`` bf16
+    with w the log-decay."""
+    D = int(H) * HEAD_SIZE
+    T = int(k.shape[0]) if k.dim() == 2 else -1
+    shape = (T, D)
+    k = _bf16_2d(k, "k", shape)
+    dev = k.device
+    v, w_lora, a_lora = (_bf16_2d(t, n, shape) for t, n in
+                         ((v, "v"), (w_lora, "w_lora"), (a_lora, "a_lora")))
+    k_k = _bf16_2d(k_k.reshape(-1), "k_k", (D,))
+    k_a = _bf16_2d(k_a.reshape(-1), "k_a", (D,))
+    if (v_lora is None) != (v_first is None):
+        raise ValueError("v_lora and v_first go together")
+    if v_lora is not None:
+        v_lora = _bf16_2d(v_lora, "v_lora", shape)
+        v_first = _bf16_2d(v_first, "v_first", shape)
+    for t in (v, w_lora, a_lora, k_k, k_a) + (() if v_lora is None else (v_lora, v_first)):
+        if t.device != dev:
+            raise ValueError("time-mix inputs must share a device")
+    outs = torch.empty((5, T, D), dtype=torch.bfloat16, device=dev)
+    if T == 0:
+        return tuple(outs)
+    rc = _lib.load().wkv7_time_mix_inputs(T, int(H), k.data_ptr(), v.data_ptr(),
+                                          w_lora.data_ptr(), a_lora.data_ptr(), _ptr(v_lora),
+                                          _ptr(v_first), k_k.data_ptr(), k_a.data_ptr(),
+                                          *[o.data_ptr() for o in outs], _stream_ptr(dev))
+    _lib.check(rc, "wkv7_time_mix_inputs")
+    return tuple(outs)
+
+
+def time_mix_output(H: int, y, r, k, v, g, r_k, ln_w, ln_b, eps: float,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head GroupNorm of the WKV output ``y [T, H, 64]`` (bf16 or fp32)
+    plus the bonus term ``(sum r k r_k) v``, times the gate ``g``; every other
+    tensor ``[T, H*64]`` bf16, ``r_k``/``ln_w``/``ln_b`` ``[H*64]``. Returns
+    the output projection's input ``[T, H*64]`` bf16."""
+    D = int(H) * HEAD_SIZE
+    _require_cuda(y, "y")
+    T = int(y.shape[0])
+    if tuple(y.shape) not in ((T, int(H), HEAD_SIZE), (T, D)):
+        raise ValueError(f"y must be [T, {H}, 64], got {tuple(y.shape)}")
+    code = _y_code(y.dtype)
+    y = y.contiguous()
+    if y.data_ptr() % 16:
+        y = y.clone()
+    dev = y.device
+    r, k, v, g = (_bf16_2d(t, n, (T, D)) for t, n in ((r, "r"), (k, "k"), (v, "v"), (g, "g")))
+    r_k, ln_w, ln_b = (_bf16_2d(t.reshape(-1), n, (D,)) for t, n in
+                       ((r_k, "r_k"), (ln_w, "ln_w"), (ln_b, "ln_b")))
+    for t in (r, k, v, g, r_k, ln_w, ln_b):
+        if t.device != dev:
+            raise ValueError("time-mix output tensors must share a device")
+    o = _out(out, (T, D), torch.bfloat16, dev, "out")
+    if T == 0:
+        return o
+    rc = _lib.load().wkv7_time_mix_output(T, int(H), y.data_ptr(), code, r.data_ptr(),
+                                          k.data_ptr(), v.data_ptr(), g.data_ptr(),
+                                          r_k.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(),
+                                          float(eps), o.data_ptr(), _stream_ptr(dev))
+    _lib.check(rc, "wkv7_time_mix_output")
+    return o
 
 
 # -- fla wkv-op signatures --------------------------------------------------------------
