@@ -509,6 +509,109 @@ def bench_store(torch, dev, args):
     return res
 
 
+def bench_time_mix(torch, dev, args):
+    """The RWKV-7 time-mix stages around the WKV op at the 1.5B width
+    (D = 2048, H = 32). Element-wise kernels at the config-2 token count
+    (8 x 4096 tokens), each timed alone with HIP events on the launch stream:
+      token_shift_mix  per token: x 4 KiB + 6 mixes 24 KiB (the previous row
+                       is the neighbour's x, read from cache), per sequence
+                       the slot row read + written
+      time_mix_inputs  per token: 6 inputs (k, v, w/a/v LoRA, v_first) read,
+                       5 outputs written, 4 KiB each
+      time_mix_output  per token: y, r, k, v, g read, 1 output written
+    and the whole block (shift, GEMMs, kernels, WKV, o_proj) per layer for a
+    256-slot decode step and for the 8 x 4096-token prefill."""
+    from wkvm_amd import ops
+    from wkvm_amd.layout import RWKV7StateLayout
+    from wkvm_amd.state import RWKV7StateBank
+    from wkvm_amd.timemix import RWKV7TimeMix, TimeMixDecodeGraph, TokenBatch
+
+    layout = RWKV7StateLayout.for_shape("1.5B")
+    D, H = layout.hidden_size, layout.num_heads
+    nseq, T = 8, 4096
+    N = nseq * T
+    bank = RWKV7StateBank(layout, 512, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 40)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+
+    def timed(fn, iters=10):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters * 1e3  # us
+
+    slots = list(range(1, nseq + 1))
+    cu = [i * T for i in range(nseq + 1)]
+    ids_t = torch.tensor(slots, dtype=torch.int32, device=dev)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    x = rnd(N, D)
+    mix = rnd(6, D)
+    shift_out = torch.empty((6, N, D), dtype=torch.bfloat16, device=dev)
+    k, v, wl, al, vl, vf = (rnd(N, D) for _ in range(6))
+    kk, ka = rnd(D), rnd(D)
+    y = rnd(N, H, 64)
+    r, gg = rnd(N, D), rnd(N, D)
+    rk, lw, lb = rnd(D), rnd(D), rnd(D)
+    res = {}
+    kern = {
+        "token_shift_mix": (lambda: ops.token_shift_mix(x, bank.shift[1, 0], ids_t, mix, cu_t,
+                                                        out=shift_out),
+                            N * D * 2 * 7 + nseq * D * 2 * 2),
+        "time_mix_inputs": (lambda: ops.time_mix_inputs(H, k, v, wl, al, kk, ka, vl, vf),
+                            N * D * 2 * 11),
+        "time_mix_output": (lambda: ops.time_mix_output(H, y, r, k, v, gg, rk, lw, lb, 64e-5),
+                            N * D * 2 * 6),
+    }
+    for name, (fn, nbytes) in kern.items():
+        us = timed(fn)
+        res[name] = {"us": us, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
+                     "frac_hbm_peak": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS}
+        log(f"time-mix {name}: {N} tokens x D={D}: {us:.1f} us, "
+            f"{res[name]['gbps']:.0f} GB/s ({100 * res[name]['frac_hbm_peak']:.1f} % of peak)")
+    del shift_out, k, v, wl, al, vl, vf, y, r, gg
+    # whole block, layer 1 (with the v_first lerp)
+    layer = RWKV7TimeMix.random(layout, 1, dev, seed=args.seed)
+    gen = torch.Generator().manual_seed(args.seed + 41)
+    dslots = (torch.randperm(512, generator=gen)[:256] + 1).tolist()
+    for mode, xin, batch in (
+            ("decode_256", rnd(256, D), TokenBatch.plan(bank, dslots)),
+            ("prefill_8x4096", x, TokenBatch.plan(bank, slots, cu))):
+        vfirst = rnd(int(xin.shape[0]), D)
+        us = timed(lambda: layer.forward(bank, xin, batch, vfirst), iters=5)
+        res[f"block_{mode}_us"] = us
+        log(f"time-mix block (1.5B layer, {mode}): {us:.1f} us per layer")
+    del x
+    # the whole 24-layer time-mix decode step for 256 slots: eager vs one graph
+    layers = [RWKV7TimeMix.random(layout, l, dev, seed=args.seed) for l in range(layout.n_layer)]
+    tg = TimeMixDecodeGraph(bank, layers, 256)
+    tg.set_slots(dslots)
+    tg.x.copy_(rnd(layout.n_layer, 256, D))
+    batch = TokenBatch.plan(bank, dslots)
+
+    def eager_step():
+        vf = None
+        for l, lay in enumerate(layers):
+            _, vf = lay.forward(bank, tg.x[l], batch, vf)
+
+    eager_us = timed(eager_step, iters=5)
+    graph_us = timed(tg.replay, iters=10)
+    res["decode_step_24_layers"] = {"eager_us": eager_us, "graph_us": graph_us,
+                                    "slot_steps_per_s_graph": 256 / (graph_us * 1e-6)}
+    log(f"time-mix decode step, 24 layers x 256 slots: eager {eager_us:.0f} us, graph "
+        f"{graph_us:.0f} us ({256 / (graph_us * 1e-6):.0f} slot-steps/s)")
+    del bank, tg, layers
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(args):
     """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
     slots of a 512-slot pool) for as many steps as fit ~10 s, at least one."""
@@ -639,6 +742,7 @@ def main() -> int:
         extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)
         extra["decode_graph"] = bench_decode_graph(torch, dev, args)
         extra["state_store"] = bench_store(torch, dev, args)
+        extra["time_mix"] = bench_time_mix(torch, dev, args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     line = {
         "metric": "WKV7 decode slot-steps/s + achieved HBM GB/s; chunked-prefill tokens/s",

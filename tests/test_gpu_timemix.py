@@ -221,3 +221,41 @@ def test_block_ragged_batch_equals_separate_requests(dev):
     for l in range(len(layers)):
         sep = np.concatenate([U.f64(p[l]) for p in parts])
         assert U.rel_l2(U.f64(outs[l]), sep) <= 1e-2
+
+
+def test_time_mix_decode_graph_replays_match_eager(dev):
+    """Replays of the captured all-layer time-mix decode step equal the eager
+    blocks bit for bit (outputs, shift rows, wkv state), over several steps with
+    different slot batches and unrelated eager GPU work between replays."""
+    from wkvm_amd.timemix import TimeMixDecodeGraph
+
+    layout = RWKV7StateLayout(n_layer=3, hidden_size=256, num_heads=4, head_dim=64,
+                              head_v_dim=64, dtype=torch.bfloat16)
+    eager = RWKV7StateBank(layout, 20, device=dev)
+    eager.wkv.normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(80))
+    eager.shift.copy_(_bf(eager.shift.shape, dev, 81))
+    graphed = RWKV7StateBank(layout, 20, device=dev)
+    graphed.wkv.copy_(eager.wkv)
+    graphed.shift.copy_(eager.shift)
+    layers = [RWKV7TimeMix.random(layout, l, dev, seed=5) for l in range(3)]
+    B = 6
+    tg = TimeMixDecodeGraph(graphed, layers, B)
+    gen = torch.Generator().manual_seed(82)
+    for step in range(4):
+        slots = (torch.randperm(20, generator=gen)[:B] + 1).tolist()
+        xs = _bf((3, B, 256), dev, 90 + step)
+        batch = TokenBatch.plan(eager, slots)
+        v_first, ref = None, []
+        for l, layer in enumerate(layers):
+            o, v_first = layer.forward(eager, xs[l], batch, v_first)
+            ref.append(o)
+        tg.set_slots(slots)
+        tg.x.copy_(xs)
+        out = tg.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(torch.stack(out), torch.stack(ref)), f"step {step}: outputs differ"
+        assert torch.equal(graphed.shift, eager.shift), f"step {step}: shift rows differ"
+        assert torch.equal(graphed.wkv, eager.wkv), f"step {step}: wkv state differs"
+        scratch = torch.randn(1 << 16, device=dev).sum()
+        torch.cuda.synchronize()
+        del scratch
