@@ -57,6 +57,10 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--only", choices=("fork_decode_7b", "mixed_ragged", "decode_graph",
+                                       "state_store", "time_mix"),
+                    help="run just this extra section and print its result as JSON (for "
+                         "rocprofv3 runs; not the benchmark line)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a few config-1 decode steps plus one "
                          "1 GiB slot copy (the counter calibration), then exit")
@@ -733,6 +737,14 @@ def main() -> int:
     launcher = Launcher(torch, dev)
     if args.pmc_probe:
         pmc_probe(torch, dev, args, launcher)
+        return 0
+    if args.only:
+        fn = {"fork_decode_7b": lambda: bench_fork_decode_7b(torch, dev, args, launcher),
+              "mixed_ragged": lambda: bench_mixed(torch, dev, args, launcher),
+              "decode_graph": lambda: bench_decode_graph(torch, dev, args),
+              "state_store": lambda: bench_store(torch, dev, args),
+              "time_mix": lambda: bench_time_mix(torch, dev, args)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
         return 0
     dec = bench_decode(torch, dev, args, launcher)
     pre = bench_prefill(torch, dev, args, launcher)

@@ -46,6 +46,10 @@ def _bf(shape, dev, seed, scale=1.0):
     (2048, 9, [2, 7, 4, 5, 8], [0, 5, 5, 40, 41, 57], 6),  # ragged prefill, an empty sequence
     (2048, 9, [6], [0, 1], 1),                           # one token, channel-mix family (M = 1)
     (4096, 5, [1, 3], [0, 130, 131], 6),                 # 7B width, D = 2 block passes
+    # 2-token tiles: boundaries inside tiles, a one-token sequence
+    (2048, 9, [3, 8, 1], [0, 2999, 3000, 5001], 6),
+    # 8-token tiles: boundaries at odd offsets, one-token and empty sequences
+    (2048, 9, [4, 2, 6, 7, 1, 5], [0, 1, 5003, 5003, 5006, 12001, 16390], 6),
 ])
 def test_token_shift_mix_bit_exact(dev, D, rows, slots, cu, M):
     T = len(slots) if cu is None else cu[-1]
