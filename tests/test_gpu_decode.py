@@ -193,3 +193,23 @@ def test_row_order_changes_visiting_order_only(dev):
     with pytest.raises(ValueError):
         ops.wkv7_decode_slots(base.clone(), ids_t, *vecs,
                               row_order=torch.arange(16, dtype=torch.int32, device=dev))
+
+
+def test_7b_shape_decode_matches_oracle(dev):
+    """7B head count (H = 64, config 3's shape): 48 slots scattered in a
+    160-slot pool, bf16 and fp32 y, two steps against the oracle."""
+    H, S, B = 64, 160, 48
+    gen = synthetic.make_generator(171)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = synthetic.active_slots(S, B, gen)
+    gpool = pool.to(dev)
+    for y_dtype in (torch.bfloat16, torch.float32):
+        vecs = synthetic.wkv7_vectors((B, H, 64), gen)
+        before = gpool.cpu().numpy()
+        y = ops.wkv7_decode_slots(gpool, ids, *(vecs[n].to(dev) for n in "rwkvab"),
+                                  out_dtype=y_dtype)
+        torch.cuda.synchronize()
+        _check_step(before, ids, U.vec_bits(vecs), gpool, y)
+    untouched = [i for i in range(S + 1) if i not in set(ids)]
+    assert torch.equal(gpool[untouched].cpu(), pool[untouched])

@@ -223,3 +223,22 @@ def test_mixed_step_equals_separate_calls(dev):
     with pytest.raises(ValueError, match="same step"):
         run.mixed_step([{"wkv": 1, "shift": 1}], [[x[:1] for x in d] for d in dec_in],
                        [{"wkv": 1, "shift": 1}], [1], [[x[:1] for x in p] for p in pre_in])
+
+
+@pytest.mark.parametrize("y_dtype", [torch.bfloat16, torch.float32])
+def test_7b_shape_prefill_matches_oracle(dev, y_dtype):
+    """7B head count (H = 64): ragged sequences from slot state, lengths
+    around the sub-chunk and chunk sizes."""
+    H, S = 64, 10
+    lens = [17, 300, 1, 64, 129]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    gen = synthetic.make_generator(181)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = synthetic.active_slots(S, len(lens), gen)
+    vecs = synthetic.wkv7_vectors((int(cu[-1]), H, 64), gen)
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_varlen(gpool, ids, cu.tolist(), *(vecs[n].to(dev) for n in "rwkvab"),
+                                out_dtype=y_dtype)
+    torch.cuda.synchronize()
+    _check(pool.numpy(), ids, cu, U.vec_bits(vecs), gpool, y, zero_init=False)
