@@ -78,8 +78,9 @@ class Launcher:
         self.check = _lib.check
         self.stream = torch.cuda.current_stream(dev).cuda_stream
 
-    def decode(self, pool, rows, H, ids, order, B, xs, y):
-        rc = self.lib.wkv7_decode_slots(pool, rows, H, ids, order, B, *xs, y, 0, 1.0, self.stream)
+    def decode(self, pool, rows, H, ids, order, B, xs, y, stream=None):
+        rc = self.lib.wkv7_decode_slots(pool, rows, H, ids, order, B, *xs, y, 0, 1.0,
+                                        self.stream if stream is None else stream)
         if rc:
             self.check(rc, "wkv7_decode_slots")
 
@@ -320,7 +321,8 @@ def bench_fork_decode_7b(torch, dev, args, launcher):
 def bench_mixed(torch, dev, args, launcher):
     """Config 4: 1.5B, 1024-slot pool; 64 rows prefill U[1, 2048] tokens from
     zero state plus 448 rows decode one token; one decode launch and one varlen
-    prefill launch per layer, 24 layers = one scheduler step."""
+    prefill launch per layer, 24 layers = one scheduler step. Timed with the
+    decode launches on a side stream (the runner's schedule) and on one stream."""
     from wkvm_amd import ops, synthetic
 
     L, H, S, NP, ND = 24, 32, 1024, 64, 448
@@ -348,13 +350,27 @@ def bench_mixed(torch, dev, args, launcher):
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     ws_ptr = ws.data_ptr() if ws_bytes else None
 
-    def step(order=lpt_t.data_ptr(), decode=True):
+    side = torch.cuda.Stream(dev)  # default priority
+    main = torch.cuda.current_stream(dev)
+
+    def step(order=lpt_t.data_ptr(), decode=True, concurrent=False):
+        # concurrent: each layer's prefill on the main stream, then its decode
+        # on a side stream forked from and joined into the main stream
+        # (WKV7Runner.mixed_step's schedule)
+        if decode and concurrent:
+            side.wait_stream(main)
         for l in range(L):
-            if decode:
+            if decode and not concurrent:
                 launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(),
                                 dec_order.data_ptr(), ND, ptrs(dx[l]), dy.data_ptr())
             launcher.prefill(wkv[l].data_ptr(), S + 1, H, pre_t.data_ptr(), cu_t.data_ptr(), NP, T,
                              ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes, order)
+            if decode and concurrent:
+                launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(),
+                                dec_order.data_ptr(), ND, ptrs(dx[l]), dy.data_ptr(),
+                                stream=side.cuda_stream)
+        if decode and concurrent:
+            main.wait_stream(side)
 
     def timed(**kw):
         reps = 3
@@ -367,8 +383,10 @@ def bench_mixed(torch, dev, args, launcher):
         return e0.elapsed_time(e1) / reps
 
     step()
+    step(concurrent=True)
     torch.cuda.synchronize()
-    ms = timed()
+    ms_serial = timed()
+    ms = timed(concurrent=True)
     # the ragged prefill alone, longest-first vs index order of the sequences
     pre_lpt, pre_idx = timed(decode=False), timed(decode=False, order=None)
     step_bytes = L * (ND * slot_layer_bytes(H) + T * H * 7 * HEAD_VEC_B + NP * H * HEAD_STATE_B)
@@ -377,10 +395,12 @@ def bench_mixed(torch, dev, args, launcher):
         "prefill_tokens": T,
         "hbm_gbps": step_bytes / (ms * 1e-3) / 1e9,
         "tokens_per_s": (T + ND) / (ms * 1e-3),
+        "ms_per_step_single_stream": ms_serial,
         "prefill_ms_longest_first": pre_lpt,
         "prefill_ms_index_order": pre_idx,
     }
-    log(f"mixed cfg4: {ms:.2f} ms/step over 24 layers, {T} prefill tokens + {ND} decodes, "
+    log(f"mixed cfg4: {ms:.2f} ms/step over 24 layers (decode on a side stream; "
+        f"{ms_serial:.2f} ms on one stream), {T} prefill tokens + {ND} decodes, "
         f"{res['hbm_gbps']:.0f} GB/s; prefill alone {pre_lpt:.2f} ms longest-first, "
         f"{pre_idx:.2f} ms index order")
     del wkv, dx, px, dy, py, ws

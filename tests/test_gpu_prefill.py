@@ -242,3 +242,32 @@ def test_7b_shape_prefill_matches_oracle(dev, y_dtype):
                                 out_dtype=y_dtype)
     torch.cuda.synchronize()
     _check(pool.numpy(), ids, cu, U.vec_bits(vecs), gpool, y, zero_init=False)
+
+
+def test_mixed_step_concurrent_equals_serial(dev):
+    """The decode launches on a side stream (forked from and joined into the
+    current stream) give the same bits as the single-stream step."""
+    lay = RWKV7StateLayout(n_layer=3, hidden_size=512, num_heads=8, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    gen = synthetic.make_generator(62)
+    S = 40
+    init = synthetic.initial_states((3, S + 1, 8, 64, 64), gen).to(dev)
+    dec_slots = list(range(2, 34, 2))
+    pre_slots = [1, 5, 39]
+    lens = [700, 33, 1]
+    dec_in = [synthetic.order(synthetic.wkv7_vectors((16, 8, 64), gen, device=dev))
+              for _ in range(3)]
+    pre_in = [synthetic.order(synthetic.wkv7_vectors((sum(lens), 8, 64), gen, device=dev))
+              for _ in range(3)]
+    out = []
+    for concurrent in (True, False):
+        bank = RWKV7StateBank(lay, num_slots=S, device=dev)
+        bank.wkv.copy_(init)
+        ys = WKV7Runner(bank).mixed_step([{"wkv": s, "shift": s} for s in dec_slots], dec_in,
+                                         [{"wkv": s, "shift": s} for s in pre_slots], lens, pre_in,
+                                         concurrent=concurrent)
+        torch.cuda.synchronize()
+        out.append((bank.wkv.clone(), ys))
+    assert torch.equal(out[0][0], out[1][0])
+    for a, b in zip(out[0][1][0] + out[0][1][1], out[1][1][0] + out[1][1][1]):
+        assert torch.equal(a, b)
