@@ -638,7 +638,8 @@ def bench_time_mix(torch, dev, args):
 
 def cpu_baseline(args):
     """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
-    slots of a 512-slot pool) for as many steps as fit ~10 s, at least one."""
+    slots of a 512-slot pool) for as many steps as fit ~10 s, at least one;
+    then config-2 prefill (one layer, 8 sequences) for ~5 s."""
     import numpy as np
     import torch
 
@@ -673,6 +674,30 @@ def cpu_baseline(args):
                   f"with OpenMP, {el:.1f} s",
     }
     log(f"cpu baseline: {res['value']:.1f} slot-steps/s on {threads} threads ({steps} steps)")
+    del pool
+    # config-2 prefill (one layer): 8 sequences from zero state, 512-token
+    # slices of the 4096-token rows, repeated for ~5 s
+    nseq, Tp = 8, 512
+    ppool = np.zeros((nseq + 1, H, 64, 64), dtype=np.float32)
+    pv = synthetic.wkv7_vectors((nseq * Tp, H, 64), gen)
+    pbits = [pv[n].contiguous().view(torch.int16).numpy().view(np.uint16) for n in "rwkvab"]
+    cu = [i * Tp for i in range(nseq + 1)]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.port_prefill_f32(ppool, list(range(1, nseq + 1)), cu, *pbits, zero_init=reps == 0)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 5.0 or reps >= 24:
+            break
+    res["prefill"] = {
+        "value": reps * nseq * Tp / el,
+        "unit": "tokens/s per layer",
+        "sample": f"{reps} x 8 sequences x {Tp} tokens (1.5B heads, H=32), continuing through "
+                  f"the slots (up to 8 x {reps * Tp} tokens), fp32 C port with OpenMP, "
+                  f"{el:.1f} s",
+    }
+    log(f"cpu baseline prefill: {res['prefill']['value']:.0f} tokens/s per layer on {threads} "
+        f"threads")
     return res
 
 
