@@ -54,10 +54,18 @@ constexpr int kRing = 4;
 constexpr int kOpWaves = 4;                      // operand wavefronts
 constexpr int kChan = kHead / (4 * kOpWaves);  // key channels per operand lane
 constexpr int kThreads = kWave * (8 + kOpWaves);  // 4 state + operand + 4 score waves
-// LDS row pitches (in bf16 elements), padded so that the 16 rows one MFMA
-// operand load touches fall in distinct banks: 144 B rows for the 64-wide
-// arrays, 40 B rows for the 16-wide ones.
-constexpr int kPR = kHead + 8;  // [row][64] arrays
+// LDS layouts. The [row][64] operand arrays have unpadded 128 B rows whose
+// 16 B chunks are XOR-swizzled by the row (chunk c of row r sits at c ^ (r & 7)):
+// the MFMA operand loads (16 rows x 4 chunks per ds_read_b128) are then free of
+// bank conflicts on gfx950, which 144 B padded rows are not (measured with the
+// LDS bank-conflict counters). The [j][s] arrays keep 80 B rows (their 2-byte
+// transposing stores are conflict-free there and conflict at every pitch that
+// frees their loads).
+constexpr int kPR = kHead;  // [row][64] arrays: 128 B rows, chunk-swizzled
+// element offset of key-position element e (0..63) of row r of a [row][64] array
+__device__ __forceinline__ int rk_off(int r, int e) {
+  return r * kPR + ((((e >> 3) ^ r) & 7) << 3) + (e & 7);
+}
 constexpr int kPQ = 2 * kSub + 8;  // [row][4 token groups][8] arrays (80 B rows)
 constexpr int kPG = kHead + 4;     // gam rows (floats)
 
@@ -245,7 +253,7 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
   }
 
   const int c0 = kChan * (4 * part + cg);  // key channels c0 .. c0+kChan-1 (consecutive key_pos)
-  const int ro = t * kPR + key_pos(c0);
+  const int ro = rk_off(t, key_pos(c0));  // kChan consecutive elements inside one chunk
   st_pairs(&S.A[0][ro], ah);
   st_pairs(&S.A[1][ro], al);
   st_pairs(&S.R[0][ro], rh);
@@ -282,7 +290,7 @@ __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, in
   f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    const int off = li * kPR + 32 * kb + 8 * lg;
+    const int off = rk_off(li, 32 * kb + 8 * lg);
     d = mma32x3(ld16(Y + off), ld16(Y + kLo + off), ld16(X + off), ld16(X + kLo + off), d);
   }
   // d[r] = M[t = li][s = 4lg + r]; L_* keep s < t, M_* keep s <= t
@@ -346,7 +354,7 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   uint4 ah[2], al[2], rh[2], rl[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    const int off = li * kPR + 32 * kb + 8 * lg;
+    const int off = rk_off(li, 32 * kb + 8 * lg);
     ah[kb] = ld16(&S.A[0][off]);
     al[kb] = ld16(&S.A[1][off]);
     rh[kb] = ld16(&S.R[0][off]);
