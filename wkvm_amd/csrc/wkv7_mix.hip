@@ -30,6 +30,7 @@ struct Bf8 {
   uint32_t p[4];  // 8 bf16, element 2i in the low half of p[i]
 };
 
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ Bf8 ld8(const uint16_t* p) {
   const uint4 v = *reinterpret_cast<const uint4*>(p);
   return Bf8{{v.x, v.y, v.z, v.w}};
@@ -37,6 +38,7 @@ __device__ __forceinline__ Bf8 ld8(const uint16_t* p) {
 __device__ __forceinline__ void st8(uint16_t* p, const Bf8& v) {
   *reinterpret_cast<uint4*>(p) = make_uint4(v.p[0], v.p[1], v.p[2], v.p[3]);
 }
+
 __device__ __forceinline__ float el(const Bf8& v, int e) {
   return (e & 1) ? bf16_hi(v.p[e >> 1]) : bf16_lo(v.p[e >> 1]);
 }
@@ -102,8 +104,15 @@ __device__ __forceinline__ Bf4 ld4(const uint16_t* p) {
   const uint2 v = *reinterpret_cast<const uint2*>(p);
   return Bf4{{v.x, v.y}};
 }
+// Rows streamed once by time_mix_inputs / time_mix_output are read and written
+// with non-temporal hints (9-10 % faster than plain accesses; the token shift's
+// outputs are not: non-temporal stores made it 7 % slower).
+__device__ __forceinline__ Bf4 ld4_nt(const uint16_t* p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  return Bf4{{v.x, v.y}};
+}
 __device__ __forceinline__ void st4(uint16_t* p, float a, float b, float c, float d) {
-  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16(a, b), pack_bf16(c, d));
+  __builtin_nontemporal_store(u32x2_t{pack_bf16(a, b), pack_bf16(c, d)}, reinterpret_cast<u32x2_t*>(p));
 }
 __device__ __forceinline__ float el(const Bf4& v, int e) {
   return (e & 1) ? bf16_hi(v.p[e >> 1]) : bf16_lo(v.p[e >> 1]);
@@ -138,7 +147,8 @@ __global__ __launch_bounds__(kMixThreads) void time_mix_inputs_kernel(int64_t un
   const int64_t h = unit % H;
   const int64_t o = unit * kHead + 4 * sub;  // element offset: token row, head, channels
   const int pc = int(h * kHead + 4 * sub);   // parameter offset (channel within D)
-  const Bf4 k = ld4(in.k + o), v = ld4(in.v + o), wl = ld4(in.w_lora + o), al = ld4(in.a_lora + o);
+  const Bf4 k = ld4_nt(in.k + o), v = ld4_nt(in.v + o), wl = ld4_nt(in.w_lora + o),
+            al = ld4_nt(in.a_lora + o);
   const Bf4 kk_s = ld4(in.k_k + pc), ka = ld4(in.k_a + pc);
   float kk[4], a[4], ssq = 0.f;
 #pragma unroll
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(kMixThreads) void time_mix_inputs_kernel(int64_t un
     vv[e] = el(v, e);
   }
   if (in.v_lora) {  // uniform: lerp(v, v_first, sigmoid(v_lora)) for layers > 0
-    const Bf4 vl = ld4(in.v_lora + o), vf = ld4(in.v_first + o);
+    const Bf4 vl = ld4_nt(in.v_lora + o), vf = ld4_nt(in.v_first + o);
 #pragma unroll
     for (int e = 0; e < 4; ++e) vv[e] = fmaf(el(vf, e) - vv[e], sigmoidf(el(vl, e)), vv[e]);
   }
@@ -192,11 +202,11 @@ __global__ __launch_bounds__(kMixThreads) void time_mix_output_kernel(int64_t un
     const float4 yv = *reinterpret_cast<const float4*>(static_cast<const float*>(in.y) + o);
     y[0] = yv.x; y[1] = yv.y; y[2] = yv.z; y[3] = yv.w;
   } else {
-    const Bf4 yv = ld4(static_cast<const uint16_t*>(in.y) + o);
+    const Bf4 yv = ld4_nt(static_cast<const uint16_t*>(in.y) + o);
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = el(yv, e);
   }
-  const Bf4 r = ld4(in.r + o), k = ld4(in.k + o), v = ld4(in.v + o), g = ld4(in.g + o);
+  const Bf4 r = ld4_nt(in.r + o), k = ld4_nt(in.k + o), v = ld4_nt(in.v + o), g = ld4_nt(in.g + o);
   const Bf4 rk = ld4(in.r_k + pc), lw = ld4(in.ln_w + pc), lb = ld4(in.ln_b + pc);
   float sum = 0.f, bonus = 0.f;
 #pragma unroll
