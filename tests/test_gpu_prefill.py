@@ -271,3 +271,34 @@ def test_mixed_step_concurrent_equals_serial(dev):
     assert torch.equal(out[0][0], out[1][0])
     for a, b in zip(out[0][1][0] + out[0][1][1], out[1][1][0] + out[1][1][1]):
         assert torch.equal(a, b)
+
+
+def test_large_batch_uses_the_64bit_input_path(dev):
+    """A batch whose input bytes exceed 31-bit offsets (H = 64, 262,444 tokens)
+    runs the operand waves' global-load path instead of the buffer-resource
+    one; the first (checked) sequence must match the oracle there too. The
+    second sequence is zero input and only makes the batch large."""
+    H, S = 64, 4
+    lens = [300, 262144]
+    cu = [0, 300, 300 + 262144]
+    gen = synthetic.make_generator(191)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    small = synthetic.wkv7_vectors((lens[0], H, 64), gen)
+    xs = []
+    for n in "rwkvab":
+        t = torch.zeros((cu[-1], H, 64), dtype=torch.bfloat16, device=dev)
+        t[:lens[0]] = small[n].to(dev)
+        xs.append(t)
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_varlen(gpool, [2, 3], cu, *xs, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.scan_bf16(np.array([0, lens[0]]), *U.vec_bits(small), pool=pool.numpy(),
+                               slot_ids=[2])
+    assert U.rel_l2(U.f64(y[:lens[0]]), y_ref) <= REL_L2
+    assert U.rel_l2(U.f64(gpool[2]), h_ref[0]) <= REL_L2
+    # all-zero input: log-decay 0 is a decay of 1 and every update term is a
+    # product with zero, so the second slot keeps its state and reads out 0
+    assert not torch.any(y[lens[0]:])
+    assert U.rel_l2(U.f64(gpool[3]), pool[3].double().numpy()) <= 1e-6
+    assert torch.equal(gpool[[0, 1, 4]].cpu(), pool[[0, 1, 4]])

@@ -41,6 +41,8 @@
 // rows take the k labels of a 32-row block in the order the state tiles hold
 // them (key_pos below), so the state is a B operand straight from registers
 // as well.
+#include <type_traits>
+
 #include "wkv7_common.h"
 
 namespace wkv7 {
@@ -214,12 +216,15 @@ __device__ __forceinline__ void st_pairs(uint16_t* p, const uint32_t (&x)[N]) {
 }
 
 // Operands of sub-chunk j for key channels [4 kChan part, 4 kChan (part + 1)).
+// kMask: padding tokens arrive as copies of the last real token and are zeroed
+// here; without it the loader has already delivered them as zeros.
+template <bool kMask>
 __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int64_t j,
                                                const SeqGeom& g, int lane, int part, float scale) {
   constexpr int P = kChan / 2;
   Slot& S = sm.slot[j & (kRing - 1)];
   const int t = lane & 15, cg = lane >> 4;
-  const bool valid = g.t_beg + kSub * j + t < g.t_end;
+  const bool valid = !kMask || g.t_beg + kSub * j + t < g.t_end;
   // r and v of padding tokens only meet zero rows and columns (their k, b
   // and a are zero, and their y is not stored), so they need no masking.
   uint32_t wv[P], kv[P], av[P], bv[P];
@@ -454,11 +459,77 @@ __device__ __forceinline__ void end_tick() {
 
 // One tick of an operand wave: operands of sub-chunk k+3 (from `cur`, which
 // is then refilled with k+5).
-__device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Inputs& in,
+template <bool kMask, class Load>
+__device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Load& load,
                                           const SeqGeom& g, int lane, int part, float scale) {
-  stage_operands(sm, cur, k + 3, g, lane, part, scale);
-  load_sub(cur, in, g, k + 5, lane, part);
+  stage_operands<kMask>(sm, cur, k + 3, g, lane, part, scale);
+  load(cur, k + 5);
   end_tick();
+}
+
+// Operand waves' input loads through one buffer resource per input, based at
+// this (sequence, head)'s first token and sized to the sequence: the lane
+// offset advances by one sub-chunk per tick, and loads past the sequence end
+// return zeros (the padding tokens), so nothing is masked and no 64-bit
+// address is formed per tick. Used when every offset fits 31 bits.
+struct BufLoad {
+  __amdgpu_buffer_rsrc_t r, w, k, v, a, b;
+  uint32_t loff, step;
+  __device__ __forceinline__ void operator()(SubIn& d, int64_t j) const {
+    const int off = static_cast<int>(loff + static_cast<uint32_t>(j) * step);
+    if constexpr (kChan == 4) {
+      auto ld = [&](uint32_t (&dst)[2], __amdgpu_buffer_rsrc_t rs) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+        dst[0] = x[0];
+        dst[1] = x[1];
+      };
+      ld(d.r, r); ld(d.w, w); ld(d.k, k); ld(d.v, v); ld(d.a, a); ld(d.b, b);
+    } else {
+      d.r[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+      d.w[0] = __builtin_amdgcn_raw_buffer_load_b32(w, off, 0, 0);
+      d.k[0] = __builtin_amdgcn_raw_buffer_load_b32(k, off, 0, 0);
+      d.v[0] = __builtin_amdgcn_raw_buffer_load_b32(v, off, 0, 0);
+      d.a[0] = __builtin_amdgcn_raw_buffer_load_b32(a, off, 0, 0);
+      d.b[0] = __builtin_amdgcn_raw_buffer_load_b32(b, off, 0, 0);
+    }
+  }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const uint16_t* x, const SeqGeom& g) {
+  const uint16_t* base = x + g.t_beg * g.tstride + g.hoff;
+  const uint32_t bytes = static_cast<uint32_t>((g.t_end - g.t_beg) * g.tstride * 2);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// The operand waves' pipeline: three fill ticks, then one tick per sub-chunk.
+// Two ticks per iteration so each input buffer keeps its registers (sub-chunk
+// k+3 of tick k is in p1 for even k, p0 for odd k). The loop has a single back
+// edge, after the p0 refill: the compiler's memory-wait placement then knows
+// that p0's loads are younger than p1's and waits for p1 alone.
+template <bool kMask, class Load>
+__device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const SeqGeom& g,
+                                             int64_t n_sub, int lane, int part, float scale) {
+  SubIn p0, p1;
+  ld(p0, 0);
+  ld(p1, 1);
+  // fill ticks -3 .. -1 (stages of sub-chunks past the end, if any, work on
+  // zero tokens and are never consumed)
+  stage_operands<kMask>(sm, p0, 0, g, lane, part, scale);
+  ld(p0, 2);
+  __syncthreads();
+  stage_operands<kMask>(sm, p1, 1, g, lane, part, scale);
+  ld(p1, 3);
+  __syncthreads();
+  stage_operands<kMask>(sm, p0, 2, g, lane, part, scale);
+  ld(p0, 4);
+  __syncthreads();
+  int64_t k = 0;
+  for (; k + 1 < n_sub; k += 2) {
+    prep_tick<kMask>(sm, p1, k, ld, g, lane, part, scale);
+    prep_tick<kMask>(sm, p0, k + 1, ld, g, lane, part, scale);
+  }
+  if (k < n_sub) prep_tick<kMask>(sm, p1, k, ld, g, lane, part, scale);
 }
 
 // Twelve wavefronts in three kinds: waves 0-3 run the state chain (wave q
@@ -468,7 +539,7 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
 // holds one wave of each kind, so the hardware interleaves the state chain's
 // MFMA latencies with the operand and score work. All kinds pass the same
 // sequence of barriers: three fill ticks, then one per sub-chunk.
-template <bool kF32Out>
+template <bool kF32Out, bool kBuf>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ seq_order, int nseq,
@@ -535,31 +606,17 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   } else if (n_sub > 0) {
     // ---- operands ahead of the chain ----
     const int part = wave - 4;
-    SubIn p0, p1;
-    load_sub(p0, in, g, 0, lane, part);
-    load_sub(p1, in, g, 1, lane, part);
-    // fill ticks -3 .. -1 (stages of sub-chunks past the end, if any, work
-    // on zero tokens and are never consumed)
-    stage_operands(sm, p0, 0, g, lane, part, scale);
-    load_sub(p0, in, g, 2, lane, part);
-    __syncthreads();
-    stage_operands(sm, p1, 1, g, lane, part, scale);
-    load_sub(p1, in, g, 3, lane, part);
-    __syncthreads();
-    stage_operands(sm, p0, 2, g, lane, part, scale);
-    load_sub(p0, in, g, 4, lane, part);
-    __syncthreads();
-    // two ticks per iteration so each input buffer keeps its registers
-    // (sub-chunk k+3 of tick k is in p1 for even k, p0 for odd k). The loop
-    // has a single back edge, after the p0 refill: the compiler's memory-wait
-    // placement then knows that p0's loads are younger than p1's and waits
-    // for p1 alone.
-    int64_t k = 0;
-    for (; k + 1 < n_sub; k += 2) {
-      prep_tick(sm, p1, k, in, g, lane, part, scale);
-      prep_tick(sm, p0, k + 1, in, g, lane, part, scale);
+    if constexpr (kBuf) {
+      const BufLoad ld{seq_rsrc(in.r, g), seq_rsrc(in.w, g), seq_rsrc(in.k, g),
+                       seq_rsrc(in.v, g), seq_rsrc(in.a, g), seq_rsrc(in.b, g),
+                       2u * (uint32_t(lane & 15) * uint32_t(g.tstride) +
+                             uint32_t(kChan * (4 * part + (lane >> 4)))),
+                       2u * uint32_t(kSub) * uint32_t(g.tstride)};
+      operand_loop<false>(sm, ld, g, n_sub, lane, part, scale);
+    } else {
+      const auto ld = [&](SubIn& d, int64_t j) { load_sub(d, in, g, j, lane, part); };
+      operand_loop<true>(sm, ld, g, n_sub, lane, part, scale);
     }
-    if (k < n_sub) prep_tick(sm, p1, k, in, g, lane, part, scale);
   }
 }
 
@@ -599,13 +656,21 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
   if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
   hipStream_t s = as_stream(stream);
   const Inputs in{r, w, k, v, a, b};
-  if (y_dtype == WKV7_Y_F32)
-    prefill_chunked_kernel<true><<<unsigned(blocks), kThreads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq, in, y, total_tokens,
-        zero_init, scale);
-  else
-    prefill_chunked_kernel<false><<<unsigned(blocks), kThreads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq, in, y, total_tokens,
-        zero_init, scale);
+  // Buffer-resource input loads need every byte offset of a sequence (plus the
+  // look-ahead past its end) to fit 31 bits.
+  const bool buf = (total_tokens + 6 * kSub) * int64_t(H) * kHead * 2 < (int64_t(1) << 31);
+  auto launch = [&](auto f32, auto bufc) {
+    prefill_chunked_kernel<decltype(f32)::value, decltype(bufc)::value>
+        <<<unsigned(blocks), kThreads, 0, s>>>(wkv_layer, num_rows, H, slot_ids, cu_seqlens,
+                                               seq_order, nseq, in, y, total_tokens, zero_init,
+                                               scale);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (y_dtype == WKV7_Y_F32) {
+    if (buf) launch(T_{}, T_{}); else launch(T_{}, F_{});
+  } else {
+    if (buf) launch(F_{}, T_{}); else launch(F_{}, F_{});
+  }
   return launch_status();
 }
