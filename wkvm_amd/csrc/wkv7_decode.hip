@@ -8,8 +8,9 @@
 //   p_i = sum_j a_j h[j][i]            (before the update)
 //   h'[j][i] = d_j h[j][i] + b_j p_i + k_j v_i
 //   y_i = sum_j (scale r_j) h'[j][i]
-// The per-token vectors (decay d = exp(w), b, k, scale*r, a) are staged in LDS
-// once per workgroup. State traffic is pure streaming (32 KiB per head, read
+// Each wave stages the per-token vectors of its key rows (decay d = exp(w), b,
+// k, scale*r, a) in LDS; the partial sums of p and of y use separate LDS
+// arrays, so a workgroup passes two barriers. State traffic is pure streaming (32 KiB per head, read
 // once and written once), issued with non-temporal hints. Workgroups visit the
 // batch rows in the caller's `row_order` (slot-sorted order keeps the HBM
 // access stream inside a few neighbouring slot regions at a time).
@@ -30,7 +31,8 @@ __global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
     const uint16_t* __restrict__ b, void* __restrict__ y, float scale) {
   __shared__ float4 s_dbkr[kHead];            // (decay, b, k, scale*r) per key row j
   __shared__ float s_a[kHead];
-  __shared__ float s_part[kDecWaves][kHead];  // per-wave partial p, then partial y
+  __shared__ float s_p[kDecWaves][kHead];  // per-wave partial p
+  __shared__ float s_y[kDecWaves][kHead];  // per-wave partial y
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -50,25 +52,27 @@ __global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
   for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hp + j * kHead);
 
   const int64_t io = (row * H + head) * kHead + lane;
-  if (wave == 0) {
-    s_dbkr[lane] = make_float4(expf(bf16_to_f32(w[io])), bf16_to_f32(b[io]), bf16_to_f32(k[io]),
-                               bf16_to_f32(r[io]) * scale);
-    s_a[lane] = bf16_to_f32(a[io]);
+  const int j0 = kRowsPerWave * wave;
+  // Each wave stages the vectors of its own key rows and is their only
+  // reader, so a wavefront-scope fence orders the LDS writes before the reads
+  // (no workgroup barrier).
+  if (lane < kRowsPerWave) {
+    const int64_t jo = io + j0;  // key row j0 + lane
+    s_dbkr[j0 + lane] = make_float4(expf(bf16_to_f32(w[jo])), bf16_to_f32(b[jo]),
+                                    bf16_to_f32(k[jo]), bf16_to_f32(r[jo]) * scale);
+    s_a[j0 + lane] = bf16_to_f32(a[jo]);
   }
   const float vi = bf16_to_f32(v[io]);
-  __syncthreads();
-
-  const int j0 = kRowsPerWave * wave;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   float p0 = 0.f, p1 = 0.f;
 #pragma unroll
   for (int j = 0; j < kRowsPerWave; j += 2) {
     p0 = fmaf(s_a[j0 + j], h[j], p0);
     p1 = fmaf(s_a[j0 + j + 1], h[j + 1], p1);
   }
-  s_part[wave][lane] = p0 + p1;
+  s_p[wave][lane] = p0 + p1;
   __syncthreads();
-  const float p = (s_part[0][lane] + s_part[1][lane]) + (s_part[2][lane] + s_part[3][lane]);
-  __syncthreads();  // partial p read by every wave before it is overwritten
+  const float p = (s_p[0][lane] + s_p[1][lane]) + (s_p[2][lane] + s_p[3][lane]);
 
   float y0 = 0.f, y1 = 0.f;
 #pragma unroll
@@ -81,10 +85,10 @@ __global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
     else
       y0 = fmaf(c.w, hn, y0);
   }
-  s_part[wave][lane] = y0 + y1;
+  s_y[wave][lane] = y0 + y1;
   __syncthreads();
   if (wave == 0) {
-    const float yi = (s_part[0][lane] + s_part[1][lane]) + (s_part[2][lane] + s_part[3][lane]);
+    const float yi = (s_y[0][lane] + s_y[1][lane]) + (s_y[2][lane] + s_y[3][lane]);
     if (kF32Out)
       static_cast<float*>(y)[io] = yi;
     else
