@@ -302,3 +302,40 @@ def test_large_batch_uses_the_64bit_input_path(dev):
     assert not torch.any(y[lens[0]:])
     assert U.rel_l2(U.f64(gpool[3]), pool[3].double().numpy()) <= 1e-6
     assert torch.equal(gpool[[0, 1, 4]].cpu(), pool[[0, 1, 4]])
+
+
+@pytest.mark.parametrize("pattern", ["channels", "tokens", "all_max"])
+def test_decay_extremes_and_scale(dev, pattern):
+    """RWKV-7's log-decay lies in (-exp(-0.5), 0]. Both ends of that range
+    (no decay, and the strongest decay, whose 16-token products reach
+    e^{+-9.7} inside a sub-chunk) against the oracle, with scale = 1/8:
+    per key channel, per token, or the strongest decay everywhere."""
+    H, S = 2, 6
+    lens = [300, 333]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    T = int(cu[-1])
+    gen = synthetic.make_generator(77)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = [4, 2]
+    vecs = synthetic.wkv7_vectors((T, H, 64), gen)
+    wmax = -synthetic.DECAY_SCALE
+    if pattern == "channels":
+        w = torch.where(torch.arange(64) % 2 == 0, 0.0, wmax).expand(T, H, 64)
+    elif pattern == "tokens":
+        w = torch.where(torch.arange(T) % 3 == 0, 0.0, wmax)[:, None, None].expand(T, H, 64)
+    else:
+        w = torch.full((T, H, 64), wmax)
+    vecs["w"] = w.to(torch.bfloat16).contiguous()
+    scale = 0.125
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_varlen(gpool, ids, cu.tolist(), *(vecs[n].to(dev) for n in "rwkvab"),
+                                scale=scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.scan_bf16(cu, *U.vec_bits(vecs), pool=pool.numpy(), slot_ids=ids,
+                               scale=scale)
+    assert np.all(np.isfinite(U.f64(y)))
+    for s in range(len(ids)):
+        sl = slice(int(cu[s]), int(cu[s + 1]))
+        assert U.rel_l2(U.f64(y[sl]), y_ref[sl]) <= REL_L2
+        assert U.rel_l2(U.f64(gpool[ids[s]]), h_ref[s]) <= REL_L2
