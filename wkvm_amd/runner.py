@@ -58,11 +58,17 @@ class WKV7Runner:
         ys = [torch.empty((T, H, 64), dtype=out_dtype, device=self.device)
               for _ in layer_inputs]
         ids = ops.device_ids([slots["wkv"]], self.bank.num_slots + 1, self.device, "slots")
+        # device plans (offsets 0, n and the one-sequence order), uploaded once
+        # per chunk length rather than once per layer
+        plans: dict[int, torch.Tensor] = {}
         for start in range(0, T, self.prefill_chunk):
             n = min(self.prefill_chunk, T - start)
+            if n not in plans:
+                plans[n] = torch.tensor([0, n, 0], dtype=torch.int32, device=self.device)
+            plan = plans[n]
             for layer, xs in enumerate(layer_inputs):
-                self.bank.prefill_wkv(layer, ids, [0, n], *(x[start:start + n] for x in xs),
-                                      out=ys[layer][start:start + n])
+                self.bank.prefill_wkv(layer, ids, plan[:2], *(x[start:start + n] for x in xs),
+                                      out=ys[layer][start:start + n], seq_order=plan[2:])
         return ys
 
     @torch.inference_mode()
@@ -112,7 +118,10 @@ class WKV7Runner:
         pre_ids = ops.device_ids(ops.ids_list(prefill_batch, "wkv"), rows, self.device, "prefill")
         if set(ops.ids_list(decode_batch, "wkv")) & set(ops.ids_list(prefill_batch, "wkv")):
             raise ValueError("a slot cannot decode and prefill in the same step")
-        cu_t = torch.tensor(cu, dtype=torch.int32, device=self.device)
+        # offsets and the longest-first start order in one upload
+        nseq = len(prefill_batch)
+        plan = torch.tensor(cu + ops.longest_first(cu), dtype=torch.int32, device=self.device)
+        cu_t, pre_order = plan[:nseq + 1], plan[nseq + 1:]
         L = self.bank.layout.n_layer
         side = None
         if concurrent and decode_batch and prefill_batch:
@@ -126,7 +135,8 @@ class WKV7Runner:
             if prefill_batch:
                 pre_ys[layer] = self.bank.prefill_wkv(layer, pre_ids, cu_t,
                                                       *prefill_inputs[layer],
-                                                      zero_init=zero_init, out_dtype=out_dtype)
+                                                      zero_init=zero_init, out_dtype=out_dtype,
+                                                      seq_order=pre_order)
             if decode_batch:
                 with torch.cuda.stream(side) if side is not None else _nullcontext():
                     dec_ys[layer] = self.bank.decode_wkv(layer, dec_ids, *decode_inputs[layer],
