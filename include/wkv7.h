@@ -117,6 +117,11 @@ int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
  *   workspace     device scratch of at least
  *                 wkv7_prefill_workspace_bytes(H, nseq, total_tokens) bytes
  *                 (may be NULL when that size is 0)
+ *
+ * Decay range: the chunked form scales operands by exp(+-G) with G a sum of
+ * up to 16 consecutive log-decays, so every w must be >= -5 (exp(80) is
+ * within fp32 and bf16 range; RWKV-7's w lies in (-0.61, 0]). Stronger
+ * decays overflow to inf/NaN; the decode step has no such limit.
  */
 int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
                         const int32_t *slot_ids, const int32_t *cu_seqlens,

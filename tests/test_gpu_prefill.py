@@ -304,12 +304,13 @@ def test_large_batch_uses_the_64bit_input_path(dev):
     assert torch.equal(gpool[[0, 1, 4]].cpu(), pool[[0, 1, 4]])
 
 
-@pytest.mark.parametrize("pattern", ["channels", "tokens", "all_max"])
+@pytest.mark.parametrize("pattern", ["channels", "tokens", "all_max", "limit"])
 def test_decay_extremes_and_scale(dev, pattern):
     """RWKV-7's log-decay lies in (-exp(-0.5), 0]. Both ends of that range
     (no decay, and the strongest decay, whose 16-token products reach
     e^{+-9.7} inside a sub-chunk) against the oracle, with scale = 1/8:
-    per key channel, per token, or the strongest decay everywhere."""
+    per key channel, per token, or the strongest decay everywhere; and the
+    documented limit of the chunked form, w = -5 everywhere (e^{+-80})."""
     H, S = 2, 6
     lens = [300, 333]
     cu = np.concatenate([[0], np.cumsum(lens)])
@@ -324,8 +325,10 @@ def test_decay_extremes_and_scale(dev, pattern):
         w = torch.where(torch.arange(64) % 2 == 0, 0.0, wmax).expand(T, H, 64)
     elif pattern == "tokens":
         w = torch.where(torch.arange(T) % 3 == 0, 0.0, wmax)[:, None, None].expand(T, H, 64)
-    else:
+    elif pattern == "all_max":
         w = torch.full((T, H, 64), wmax)
+    else:
+        w = torch.full((T, H, 64), -5.0)
     vecs["w"] = w.to(torch.bfloat16).contiguous()
     scale = 0.125
     gpool = pool.to(dev)
