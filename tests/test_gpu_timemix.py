@@ -263,3 +263,30 @@ def test_time_mix_decode_graph_replays_match_eager(dev):
         scratch = torch.randn(1 << 16, device=dev).sum()
         torch.cuda.synchronize()
         del scratch
+
+
+def test_block_side_streams_give_the_same_bytes(dev):
+    """The block's independent GEMM chains on side streams (eager) produce the
+    same outputs and state as the single-stream block."""
+    layout = RWKV7StateLayout(n_layer=2, hidden_size=256, num_heads=4, head_dim=64,
+                              head_v_dim=64, dtype=torch.bfloat16)
+    banks = [RWKV7StateBank(layout, 12, device=dev) for _ in range(2)]
+    banks[0].wkv.normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(95))
+    banks[0].shift.copy_(_bf(banks[0].shift.shape, dev, 96))
+    banks[1].wkv.copy_(banks[0].wkv)
+    banks[1].shift.copy_(banks[0].shift)
+    layers = [RWKV7TimeMix.random(layout, l, dev, seed=7) for l in range(2)]
+    streams = [torch.cuda.Stream(dev) for _ in range(3)]
+    slots = [3, 7, 1, 11, 5]
+    x = _bf((2, len(slots), 256), dev, 97)
+    outs = []
+    for bank, st in zip(banks, (None, streams)):
+        batch = TokenBatch.plan(bank, slots)
+        v_first, o = None, []
+        for l, layer in enumerate(layers):
+            y, v_first = layer.forward(bank, x[l], batch, v_first, streams=st)
+            o.append(y)
+        outs.append(torch.stack(o))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(banks[0].wkv, banks[1].wkv) and torch.equal(banks[0].shift, banks[1].shift)

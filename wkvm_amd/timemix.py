@@ -131,22 +131,55 @@ class RWKV7TimeMix:
 
     def forward(self, bank: RWKV7StateBank, x: torch.Tensor, batch: TokenBatch,
                 v_first: torch.Tensor | None = None, *, zero_init: bool = False,
+                streams: list[torch.cuda.Stream] | None = None,
                 ) -> tuple[torch.Tensor, torch.Tensor]:
         """``x [T, D]`` bf16 -> ``(o [T, D] bf16, v_first)``; the slots' shift
         row ``bank.shift[l, 0]`` and wkv state ``bank.wkv[l]`` advance in
-        place. ``zero_init`` starts prefill sequences from zero wkv state."""
+        place. ``zero_init`` starts prefill sequences from zero wkv state.
+
+        ``streams`` (side streams of default priority): the projection and
+        LoRA chains are independent of one another, so they are forked onto
+        these streams after the token shift and joined before the WKV inputs.
+        At decode batch sizes each of these GEMMs fills only part of the GPU,
+        and running them side by side shortens the block; the results are the
+        same bytes either way."""
         W, l, H = self.w, self.layer_idx, self.layout.num_heads
         if l > 0 and v_first is None:
             raise ValueError("layers after the first need v_first")
         xr, xw, xk, xv, xa, xg = ops.token_shift_mix(x, bank.shift[l, 0], batch.slot_ids,
                                                      W["mix"], batch.cu_seqlens)
-        r = F.linear(xr, W["r"])
-        k = F.linear(xk, W["k"])
-        v = F.linear(xv, W["v"])
-        w_l = F.linear(torch.tanh(F.linear(xw, W["w1"])), W["w2"], W["w0"])
-        a_l = F.linear(F.linear(xa, W["a1"]), W["a2"], W["a0"])
-        v_l = F.linear(F.linear(xv, W["v1"]), W["v2"], W["v0"]) if l > 0 else None
-        g = F.linear(torch.sigmoid(F.linear(xg, W["g1"])), W["g2"])
+
+        # the independent chains between the token shift and the WKV inputs
+        chains = {
+            "r": lambda: F.linear(xr, W["r"]),
+            "k": lambda: F.linear(xk, W["k"]),
+            "v": lambda: F.linear(xv, W["v"]),
+            "w_l": lambda: F.linear(torch.tanh(F.linear(xw, W["w1"])), W["w2"], W["w0"]),
+            "a_l": lambda: F.linear(F.linear(xa, W["a1"]), W["a2"], W["a0"]),
+            "g": lambda: F.linear(torch.sigmoid(F.linear(xg, W["g1"])), W["g2"]),
+        }
+        if l > 0:
+            chains["v_l"] = lambda: F.linear(F.linear(xv, W["v1"]), W["v2"], W["v0"])
+        res: dict[str, torch.Tensor] = {}
+        if streams:
+            main = torch.cuda.current_stream(x.device)
+            lanes = [main] + list(streams)
+            for s in streams:
+                s.wait_stream(main)
+            for i, (name, fn) in enumerate(chains.items()):
+                with torch.cuda.stream(lanes[i % len(lanes)]):
+                    res[name] = fn()
+            for s in streams:
+                main.wait_stream(s)
+            if not torch.cuda.is_current_stream_capturing():
+                # made on the side streams, used and freed on this one
+                for t in res.values():
+                    t.record_stream(main)
+        else:
+            for name, fn in chains.items():
+                res[name] = fn()
+        r, k, v, w_l, a_l, g = (res[n] for n in ("r", "k", "v", "w_l", "a_l", "g"))
+        v_l = res.get("v_l")
         w, k2, v2, a, b = ops.time_mix_inputs(H, k, v, w_l, a_l, W["k_k"], W["k_a"], v_l,
                                               v_first if l > 0 else None)
         if l == 0:
@@ -176,7 +209,8 @@ class TimeMixDecodeGraph:
     batch size and to the bank's tensors (the reference's per-bucket graphs,
     experiments/m2_engine_bench.py:44-131)."""
 
-    def __init__(self, bank: RWKV7StateBank, layers: list[RWKV7TimeMix], batch_size: int):
+    def __init__(self, bank: RWKV7StateBank, layers: list[RWKV7TimeMix], batch_size: int,
+                 side_streams: int = 3):
         if batch_size < 1:
             raise ValueError("batch_size must be >= 1")
         if len(layers) < 1 or any(l.layer_idx != i for i, l in enumerate(layers)):
@@ -190,17 +224,25 @@ class TimeMixDecodeGraph:
         self.x = torch.zeros((len(layers), B, D), dtype=torch.bfloat16, device=dev)
         self.o: list[torch.Tensor] = []
         batch = TokenBatch(self.plan[:B], self.plan[2 * B:], self.plan[B:2 * B], B, B, True)
-        # initialise the BLAS handles and workspaces before capture (GEMMs
-        # only: the bank is not touched until the first replay)
-        for layer in layers:
-            for name in ("r", "k", "v", "o"):
-                _ = F.linear(self.x[0], layer.w[name])
+        # side streams (default priority) for the block's independent GEMM
+        # chains; the graph keeps their fork/join as parallel branches
+        self.streams = [torch.cuda.Stream(dev) for _ in range(side_streams)]
+        # initialise the BLAS handles and workspaces of every stream before
+        # capture (GEMMs only: the bank is not touched until the first replay)
+        main = torch.cuda.current_stream(dev)
+        for st in [main] + self.streams:
+            st.wait_stream(main)
+            with torch.cuda.stream(st):
+                for layer in layers:
+                    for name in ("r", "k", "v", "o"):
+                        _ = F.linear(self.x[0], layer.w[name])
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             v_first = None
             for l, layer in enumerate(layers):
-                out, v_first = layer.forward(bank, self.x[l], batch, v_first)
+                out, v_first = layer.forward(bank, self.x[l], batch, v_first,
+                                             streams=self.streams or None)
                 self.o.append(out)
 
     def set_slots(self, slot_ids) -> None:
