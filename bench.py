@@ -769,7 +769,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the WKV7 slot-pool path shards by slot with no "
-              "exchange step, and this build runs on a single MI355X (see DESIGN.md). "
+              "exchange step, and this build runs on a single MI355X. "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
     import torch

@@ -7,8 +7,8 @@
  * (wkvm/models/rwkv7.py:108-113) between gather/scatter copies of the pool.
  * Each entry point below replaces one of those operations; the comment on each
  * names the reference code it stands in for. The Python host package
- * `wkvm_amd` binds these symbols with ctypes; INTEGRATION.md shows the
- * binding a maintainer would add to the reference.
+ * `wkvm_amd` binds these symbols with ctypes (wkvm_amd/_lib.py lists every
+ * signature).
  *
  * Conventions (all entry points):
  *  - Memory: every pointer is caller-owned device memory (except where a
