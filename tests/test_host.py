@@ -212,3 +212,11 @@ def test_synthetic_distributions_and_determinism():
     assert len(set(ids)) == 4 and min(ids) >= 1 and max(ids) <= 16
     lens = synthetic.ragged_lengths(64, 1, 2048, synthetic.make_generator(4))
     assert min(lens) >= 1 and max(lens) <= 2048
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No CPU or eager fallback: without the built library every op raises."""
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libwkv7.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
