@@ -210,7 +210,7 @@ class TimeMixDecodeGraph:
     experiments/m2_engine_bench.py:44-131)."""
 
     def __init__(self, bank: RWKV7StateBank, layers: list[RWKV7TimeMix], batch_size: int,
-                 side_streams: int = 3):
+                 side_streams: int = 2):
         if batch_size < 1:
             raise ValueError("batch_size must be >= 1")
         if len(layers) < 1 or any(l.layer_idx != i for i, l in enumerate(layers)):
