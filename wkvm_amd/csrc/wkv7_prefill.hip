@@ -475,23 +475,26 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
 struct BufLoad {
   __amdgpu_buffer_rsrc_t r, w, k, v, a, b;
   uint32_t loff, step;
+  // kChan / 2 packed pairs of one input: an 8- or 4-byte load
+  template <int N>
+  __device__ __forceinline__ static void one(uint32_t (&dst)[N], __amdgpu_buffer_rsrc_t rs,
+                                             int off) {
+    if constexpr (N == 2) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      dst[0] = x[0];
+      dst[1] = x[1];
+    } else {
+      dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    }
+  }
   __device__ __forceinline__ void operator()(SubIn& d, int64_t j) const {
     const int off = static_cast<int>(loff + static_cast<uint32_t>(j) * step);
-    if constexpr (kChan == 4) {
-      auto ld = [&](uint32_t (&dst)[2], __amdgpu_buffer_rsrc_t rs) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
-        dst[0] = x[0];
-        dst[1] = x[1];
-      };
-      ld(d.r, r); ld(d.w, w); ld(d.k, k); ld(d.v, v); ld(d.a, a); ld(d.b, b);
-    } else {
-      d.r[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-      d.w[0] = __builtin_amdgcn_raw_buffer_load_b32(w, off, 0, 0);
-      d.k[0] = __builtin_amdgcn_raw_buffer_load_b32(k, off, 0, 0);
-      d.v[0] = __builtin_amdgcn_raw_buffer_load_b32(v, off, 0, 0);
-      d.a[0] = __builtin_amdgcn_raw_buffer_load_b32(a, off, 0, 0);
-      d.b[0] = __builtin_amdgcn_raw_buffer_load_b32(b, off, 0, 0);
-    }
+    one(d.r, r, off);
+    one(d.w, w, off);
+    one(d.k, k, off);
+    one(d.v, v, off);
+    one(d.a, a, off);
+    one(d.b, b, off);
   }
 };
 
