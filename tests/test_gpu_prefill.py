@@ -342,3 +342,36 @@ def test_decay_extremes_and_scale(dev, pattern):
         sl = slice(int(cu[s]), int(cu[s + 1]))
         assert U.rel_l2(U.f64(y[sl]), y_ref[sl]) <= REL_L2
         assert U.rel_l2(U.f64(gpool[ids[s]]), h_ref[s]) <= REL_L2
+
+
+@pytest.mark.parametrize("zero_init", [False, True])
+@pytest.mark.parametrize("y_dtype", [torch.bfloat16, torch.float32])
+def test_segmented_prefill_matches_oracle_and_one_pass(dev, zero_init, y_dtype):
+    """Sequences cut into up to 4 segments that run side by side (transition
+    runs from the identity, combined by linearity in the initial state) give
+    the oracle's y and final states, and the one-pass kernel's to fp32
+    rounding; an empty sequence and a 10-token one (a single segment) ride
+    along."""
+    H, S = 4, 10
+    lens = [700, 0, 10, 333]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    gen = synthetic.make_generator(61)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = [7, 2, 9, 4]
+    vecs = synthetic.wkv7_vectors((int(cu[-1]), H, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_segments(gpool, ids, cu.tolist(), *xs, segments=4, zero_init=zero_init,
+                                  out_dtype=y_dtype)
+    torch.cuda.synchronize()
+    _check(pool.numpy(), ids, cu, U.vec_bits(vecs), gpool, y, zero_init)
+    others = [i for i in range(S + 1) if i not in ids]
+    assert torch.equal(gpool[others].cpu(), pool[others])
+    one = pool.to(dev)
+    y1 = ops.wkv7_prefill_varlen(one, ids, cu.tolist(), *xs, zero_init=zero_init,
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert U.rel_l2(U.f64(gpool), U.f64(one)) <= 1e-5
+    if y_dtype == torch.float32:
+        assert U.rel_l2(U.f64(y), U.f64(y1)) <= 1e-5
