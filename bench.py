@@ -242,6 +242,42 @@ def bench_prefill(torch, dev, args, launcher):
         f"{res['hbm_gbps']:.0f} GB/s, MFMA {100 * res['mfma_util']:.2f} %")
     del pools, xs, ys, ws
     torch.cuda.empty_cache()
+    res["one_sequence"] = bench_prefill_one_sequence(torch, dev, args)
+    return res
+
+
+def bench_prefill_one_sequence(torch, dev, args):
+    """One long sequence (1.5B heads, 16,384 tokens, from a slot state): the
+    one-pass kernel keeps 32 compute units busy; ops.wkv7_prefill_segments
+    runs 4 segments side by side. Per-call time including the host side."""
+    from wkvm_amd import ops, synthetic
+
+    H, T = 32, 16384
+    gdev = synthetic.make_generator(args.seed + 5, dev)
+    xs = synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev))
+    pool = torch.zeros((2, H, 64, 64), dtype=torch.float32, device=dev)
+    pool.normal_(0.0, 0.1, generator=gdev)
+    y = torch.empty((T, H, 64), dtype=torch.bfloat16, device=dev)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    one = timed(lambda: ops.wkv7_prefill_varlen(pool, [1], [0, T], *xs, out=y))
+    seg = timed(lambda: ops.wkv7_prefill_segments(pool, [1], [0, T], *xs, segments=4, out=y))
+    res = {"tokens": T, "one_pass_ms": one, "segments4_ms": seg,
+           "segments4_tokens_per_s": T / (seg * 1e-3)}
+    log(f"prefill one sequence of {T} tokens (H={H}): one pass {one:.3f} ms, "
+        f"4 segments {seg:.3f} ms")
+    del xs, pool, y
+    torch.cuda.empty_cache()
     return res
 
 

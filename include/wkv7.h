@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 4
+#define WKV7_ABI_VERSION 5
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -133,6 +133,62 @@ int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
 
 /* Scratch bytes wkv7_prefill_varlen needs for this problem size. */
 size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t total_tokens);
+
+/* Run flags of wkv7_prefill_runs. */
+#define WKV7_RUN_INIT_ZERO 1      /* start from zero state */
+#define WKV7_RUN_INIT_IDENTITY 2  /* start from the identity (takes precedence) */
+#define WKV7_RUN_KV_ZERO 4        /* read k and v as zero */
+#define WKV7_RUN_Y_ALT 8          /* write y to y_alt */
+#define WKV7_RUN_STATE_ALT 16     /* slot_ids[run] is a row of state_alt, not of wkv_layer */
+
+/*
+ * wkv7_prefill_varlen over "runs" with per-run options, for the segmented
+ * prefill of few long sequences (with wkv7_segment_chain and
+ * wkv7_segment_correct below). It has no single counterpart in the reference:
+ * together the three compute what one chunk_rwkv7 call of RWKV7Runner.prefill
+ * computes (wkvm/runner/runner.py:41-63, wkvm/models/rwkv7.py:108-113), with
+ * the sequence's segments running side by side.
+ *
+ * Runs [0, n_primary) take their token ranges from cu_seqlens (as
+ * wkv7_prefill_varlen, n_primary + 1 entries); run n_primary + i takes tokens
+ * [cu_alt[2i], cu_alt[2i+1]) of the same inputs. run_flags [nseq] (device,
+ * WKV7_RUN_* bits, NULL = all 0) select the initial state, zero k and v, and
+ * redirect y to y_alt (same shape and dtype as y) and the state to
+ * state_alt [alt_rows, H, 64, 64] fp32. A run's rows must be distinct from
+ * every other run's.
+ */
+int wkv7_prefill_runs(float *wkv_layer, int64_t num_rows, int32_t H,
+                      const int32_t *slot_ids, const int32_t *cu_seqlens,
+                      const int32_t *seq_order, int32_t nseq, int64_t total_tokens,
+                      const uint16_t *r, const uint16_t *w, const uint16_t *k,
+                      const uint16_t *v, const uint16_t *a, const uint16_t *b,
+                      void *y, int32_t y_dtype, int32_t zero_init, float scale,
+                      const int32_t *run_flags, const int32_t *cu_alt, int32_t n_primary,
+                      float *state_alt, int64_t alt_rows, void *y_alt, void *stream);
+
+/*
+ * The state chain of a segmented prefill, per (sequence, head), in segment
+ * order: hin[seg] = H_in, then H_in <- state_alt[main] + state_alt[phi] H_in.
+ * H_in starts at wkv_layer[slot] (the state after segment 0) and ends there.
+ *   seq_tab  [nseq][3] int32 (device): slot, first segment, segment count
+ *   seg_tab  [nsegs][2] int32 (device): state_alt rows of the segment's zero-
+ *            state run (H0) and of its identity run (Phi)
+ *   hin      [nsegs, H, 64, 64] fp32 out: the state entering each segment
+ */
+int wkv7_segment_chain(float *wkv_layer, int64_t num_rows, int32_t H, const float *state_alt,
+                       int64_t alt_rows, const int32_t *seq_tab, int32_t nseq,
+                       const int32_t *seg_tab, int32_t nsegs, float *hin, void *stream);
+
+/*
+ * The output of a segmented prefill: for every token block,
+ * y = y0 + q hin[seg] (seg >= 0) or y = y0 (seg < 0), per head, written in
+ * y_dtype.
+ *   y0, q    [total_tokens, H, 64] fp32 (the runs' y and y_alt)
+ *   blk_tab  [nblk][3] int32 (device): first token, count (<= 64), segment
+ */
+int wkv7_segment_correct(int64_t total_tokens, int32_t H, const float *y0, const float *q,
+                         const int32_t *blk_tab, int32_t nblk, const float *hin, int32_t nsegs,
+                         void *y, int32_t y_dtype, void *stream);
 
 /*
  * Copy slot rows between two slot-indexed tensors (or within one), bit-exact.

@@ -375,3 +375,25 @@ def test_segmented_prefill_matches_oracle_and_one_pass(dev, zero_init, y_dtype):
     assert U.rel_l2(U.f64(gpool), U.f64(one)) <= 1e-5
     if y_dtype == torch.float32:
         assert U.rel_l2(U.f64(y), U.f64(y1)) <= 1e-5
+
+
+def test_runner_segmented_prefill_matches_one_pass(dev):
+    """WKV7Runner with prefill_segments: chunks of at least 2048 tokens run
+    segmented, shorter ones in one pass; every layer's y and the slot state
+    agree with the one-pass runner to fp32 rounding."""
+    lay = RWKV7StateLayout(n_layer=2, hidden_size=256, num_heads=4, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    T = 2048 + 300
+    gen = synthetic.make_generator(67)
+    inputs = [synthetic.order(synthetic.wkv7_vectors((T, 4, 64), gen, device=dev))
+              for _ in range(2)]
+    outs, finals = [], []
+    for segs in (None, 4):
+        bank = RWKV7StateBank(lay, num_slots=3, device=dev)
+        bank.wkv[:, 2].normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(68))
+        run = WKV7Runner(bank, prefill_chunk=2048, prefill_segments=segs)
+        ys = run.prefill(inputs, {"wkv": 2, "shift": 2}, out_dtype=torch.float32)
+        outs.append(torch.stack(ys))
+        finals.append(bank.wkv[:, 2].clone())
+    assert U.rel_l2(U.f64(outs[1]), U.f64(outs[0])) <= 1e-5
+    assert U.rel_l2(U.f64(finals[1]), U.f64(finals[0])) <= 1e-5

@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 4
+    assert lib.wkv7_abi_version() == 5
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():
@@ -220,3 +220,26 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load()
+
+
+def test_segment_entry_points_reject_bad_arguments():
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 4096)()
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    E_ARG, E_SHAPE = _lib.WKV7_ERR_ARG, _lib.WKV7_ERR_SHAPE
+    # runs: n_primary beyond nseq, secondary runs without ranges, misaligned inputs
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
+                                 3, None, 0, None, None) == E_ARG
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, p, None,
+                                 1, p, 2, None, None) == E_ARG
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, p + 2, *[p] * 5, p, 0, 0, 1.0,
+                                 None, None, 2, None, 0, None, None) == E_SHAPE
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 0, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
+                                 0, None, 0, None, None) == 0
+    # chain: segments without their tables; misaligned hin
+    assert lib.wkv7_segment_chain(p, 4, 2, None, 0, p, 1, None, 1, p, None) == E_ARG
+    assert lib.wkv7_segment_chain(p, 4, 2, p, 2, p, 1, p, 1, p + 4, None) == E_SHAPE
+    # correct: bad dtype, missing q with segments, misaligned fp32 y
+    assert lib.wkv7_segment_correct(8, 2, p, p, p, 1, p, 0, p, 5, None) == E_ARG
+    assert lib.wkv7_segment_correct(8, 2, p, None, p, 1, p, 1, p, 0, None) == E_ARG
+    assert lib.wkv7_segment_correct(8, 2, p, p, p, 1, p, 1, p + 8, 1, None) == E_SHAPE

@@ -22,6 +22,11 @@ WKV7_ERR_SHAPE = -2
 WKV7_ERR_WORKSPACE = -3
 WKV7_Y_BF16 = 0
 WKV7_Y_F32 = 1
+WKV7_RUN_INIT_ZERO = 1
+WKV7_RUN_INIT_IDENTITY = 2
+WKV7_RUN_KV_ZERO = 4
+WKV7_RUN_Y_ALT = 8
+WKV7_RUN_STATE_ALT = 16
 WKV7_TO_HOST = 0
 WKV7_FROM_HOST = 1
 
@@ -41,6 +46,13 @@ SIGNATURES = {
         _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
         _i32, _f32, _vp, _sz, _vp]),
     "wkv7_prefill_workspace_bytes": (_sz, [_i32, _i32, _i64]),
+    "wkv7_prefill_runs": (ctypes.c_int, [
+        _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+        _i32, _f32, _vp, _vp, _i32, _vp, _i64, _vp, _vp]),
+    "wkv7_segment_chain": (ctypes.c_int, [
+        _vp, _i64, _i32, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp]),
+    "wkv7_segment_correct": (ctypes.c_int, [
+        _i64, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp]),
     "wkv7_slot_copy": (ctypes.c_int, [
         _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
     "wkv7_slot_zero": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),

@@ -498,9 +498,11 @@ struct BufLoad {
   }
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const uint16_t* x, const SeqGeom& g) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const uint16_t* x, const SeqGeom& g,
+                                                         bool empty = false) {
   const uint16_t* base = x + g.t_beg * g.tstride + g.hoff;
-  const uint32_t bytes = static_cast<uint32_t>((g.t_end - g.t_beg) * g.tstride * 2);
+  // an empty range makes every load return zero (runs with k = v = 0)
+  const uint32_t bytes = empty ? 0u : static_cast<uint32_t>((g.t_end - g.t_beg) * g.tstride * 2);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
                                            static_cast<int>(bytes), 0x00020000);
 }
@@ -542,11 +544,25 @@ __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const S
 // holds one wave of each kind, so the hardware interleaves the state chain's
 // MFMA latencies with the operand and score work. All kinds pass the same
 // sequence of barriers: three fill ticks, then one per sub-chunk.
+// Per-run options of wkv7_prefill_runs (all absent for wkv7_prefill_varlen).
+// Runs [0, n_primary) take their token range from cu_seqlens; run
+// n_primary + i takes [ranges[2i], ranges[2i+1]). Flags select the initial
+// state (slot row, zero or identity), zero k and v, and redirect y and the
+// final state.
+struct Runs {
+  const int32_t* flags;   // [nseq] or null
+  const int32_t* cu_alt;  // [2 (nseq - n_primary)] begin/end pairs, or null
+  int32_t n_primary;
+  float* state_alt;       // [alt_rows, H, 64, 64]
+  int64_t alt_rows;
+  void* y_alt;            // like y
+};
+
 template <bool kF32Out, bool kBuf>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ seq_order, int nseq,
-    Inputs in, void* __restrict__ y, int64_t total_tokens, int zero_init, float scale) {
+    Inputs in, void* __restrict__ y, int64_t total_tokens, int zero_init, float scale, Runs runs) {
   __shared__ Shared sm;
 
   const int lane = threadIdx.x & 63;
@@ -555,11 +571,19 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   const int64_t head = blockIdx.x - pos * H;
   const int64_t seq = seq_order ? int64_t(seq_order[pos]) : pos;
   if (seq < 0 || seq >= nseq) return;  // uniform: the whole block leaves
+  const int fl = runs.flags ? runs.flags[seq] : 0;
   const int64_t slot = slot_ids[seq];
-  if (slot < 0 || slot >= num_rows) return;  // uniform: the whole block leaves
+  const int64_t rows_of = (fl & WKV7_RUN_STATE_ALT) ? runs.alt_rows : num_rows;
+  if (slot < 0 || slot >= rows_of) return;  // uniform: the whole block leaves
+  const int32_t* cu = cu_seqlens;
+  int64_t ci = seq;
+  if (seq >= runs.n_primary) {  // only with cu_alt (n_primary = nseq otherwise)
+    cu = runs.cu_alt;
+    ci = 2 * (seq - runs.n_primary);
+  }
   SeqGeom g;
-  g.t_end = min(max(int64_t(cu_seqlens[seq + 1]), int64_t(0)), total_tokens);
-  g.t_beg = min(max(int64_t(cu_seqlens[seq]), int64_t(0)), g.t_end);
+  g.t_end = min(max(int64_t(cu[ci + 1]), int64_t(0)), total_tokens);
+  g.t_beg = min(max(int64_t(cu[ci]), int64_t(0)), g.t_end);
   g.tstride = int64_t(H) * kHead;
   g.hoff = head * kHead;
   const int64_t n_sub = (g.t_end - g.t_beg + kSub - 1) / kSub;
@@ -567,15 +591,22 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   if (wave < 4) {
     // ---- state chain ----
     const int li = lane & 15, lg = lane >> 4;
-    float* hbase = wkv + (slot * H + head) * (kHead * kHead);
+    float* hbase = ((fl & WKV7_RUN_STATE_ALT) ? runs.state_alt : wkv) +
+                   (slot * H + head) * (kHead * kHead);
+    void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
     const int col0 = kSub * wave;  // this wave's value columns [col0, col0 + 16)
     // State columns of this wave as four 16x16 accumulator tiles (key blocks jb).
     f32x4 h[4];
+    const bool from_zero = zero_init || (fl & WKV7_RUN_INIT_ZERO);
+    const bool from_eye = fl & WKV7_RUN_INIT_IDENTITY;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        h[jb][rr] = zero_init ? 0.f : hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li];
+      for (int rr = 0; rr < 4; ++rr) {
+        const int j = 16 * jb + 4 * lg + rr;
+        h[jb][rr] = from_eye ? (j == col0 + li ? 1.f : 0.f)
+                             : from_zero ? 0.f : hbase[j * kHead + col0 + li];
+      }
     if (n_sub > 0) {
       end_tick();  // fill ticks
       end_tick();
@@ -584,7 +615,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
         stage_inverse(sm, k + 1, lane, wave);
-        store_y<kF32Out>(y, yv, k, g, lane, wave);
+        store_y<kF32Out>(yb, yv, k, g, lane, wave);
         end_tick();
       }
     }
@@ -610,14 +641,22 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     // ---- operands ahead of the chain ----
     const int part = wave - 4;
     if constexpr (kBuf) {
-      const BufLoad ld{seq_rsrc(in.r, g), seq_rsrc(in.w, g), seq_rsrc(in.k, g),
-                       seq_rsrc(in.v, g), seq_rsrc(in.a, g), seq_rsrc(in.b, g),
+      const bool kvz = fl & WKV7_RUN_KV_ZERO;
+      const BufLoad ld{seq_rsrc(in.r, g), seq_rsrc(in.w, g), seq_rsrc(in.k, g, kvz),
+                       seq_rsrc(in.v, g, kvz), seq_rsrc(in.a, g), seq_rsrc(in.b, g),
                        2u * (uint32_t(lane & 15) * uint32_t(g.tstride) +
                              uint32_t(kChan * (4 * part + (lane >> 4)))),
                        2u * uint32_t(kSub) * uint32_t(g.tstride)};
       operand_loop<false>(sm, ld, g, n_sub, lane, part, scale);
     } else {
-      const auto ld = [&](SubIn& d, int64_t j) { load_sub(d, in, g, j, lane, part); };
+      const bool kvz = fl & WKV7_RUN_KV_ZERO;
+      const auto ld = [&](SubIn& d, int64_t j) {
+        load_sub(d, in, g, j, lane, part);
+        if (kvz) {
+#pragma unroll
+          for (int i = 0; i < kChan / 2; ++i) d.k[i] = d.v[i] = 0u;
+        }
+      };
       operand_loop<true>(sm, ld, g, n_sub, lane, part, scale);
     }
   }
@@ -635,6 +674,43 @@ extern "C" size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t 
   return 0;
 }
 
+namespace {
+int prefill_launch(float* wkv_layer, int64_t num_rows, int32_t H, const int32_t* slot_ids,
+                   const int32_t* cu_seqlens, const int32_t* seq_order, int32_t nseq,
+                   int64_t total_tokens, const Inputs& in, void* y, int32_t y_dtype,
+                   int32_t zero_init, float scale, const Runs& runs, void* stream) {
+  const int64_t blocks = int64_t(nseq) * H;
+  if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
+  hipStream_t s = as_stream(stream);
+  // Buffer-resource input loads need every byte offset of a sequence (plus the
+  // look-ahead past its end) to fit 31 bits.
+  const bool buf = (total_tokens + 6 * kSub) * int64_t(H) * kHead * 2 < (int64_t(1) << 31);
+  auto launch = [&](auto f32, auto bufc) {
+    prefill_chunked_kernel<decltype(f32)::value, decltype(bufc)::value>
+        <<<unsigned(blocks), kThreads, 0, s>>>(wkv_layer, num_rows, H, slot_ids, cu_seqlens,
+                                               seq_order, nseq, in, y, total_tokens, zero_init,
+                                               scale, runs);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (y_dtype == WKV7_Y_F32) {
+    if (buf) launch(T_{}, T_{}); else launch(T_{}, F_{});
+  } else {
+    if (buf) launch(F_{}, T_{}); else launch(F_{}, F_{});
+  }
+  return launch_status();
+}
+
+bool inputs_aligned(const uint16_t* r, const uint16_t* w, const uint16_t* k, const uint16_t* v,
+                    const uint16_t* a, const uint16_t* b) {
+  // inputs are read as 16-byte vectors
+  const uintptr_t align = reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(w) |
+                          reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                          reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
+  return (align & 15u) == 0;
+}
+}  // namespace
+
 extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H,
                                    const int32_t* slot_ids, const int32_t* cu_seqlens,
                                    const int32_t* seq_order, int32_t nseq, int64_t total_tokens,
@@ -648,32 +724,35 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
   if (nseq == 0) return WKV7_OK;
   if (!wkv_layer || !slot_ids || !cu_seqlens) return WKV7_ERR_ARG;
   if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
-  // inputs are read as 16-byte vectors
-  const uintptr_t align = reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(w) |
-                          reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
-                          reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b);
-  if (align & 15u) return WKV7_ERR_SHAPE;
+  if (!inputs_aligned(r, w, k, v, a, b)) return WKV7_ERR_SHAPE;
   if (workspace_bytes < wkv7_prefill_workspace_bytes(H, nseq, total_tokens)) return WKV7_ERR_WORKSPACE;
   (void)workspace;
-  const int64_t blocks = int64_t(nseq) * H;
-  if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
-  hipStream_t s = as_stream(stream);
-  const Inputs in{r, w, k, v, a, b};
-  // Buffer-resource input loads need every byte offset of a sequence (plus the
-  // look-ahead past its end) to fit 31 bits.
-  const bool buf = (total_tokens + 6 * kSub) * int64_t(H) * kHead * 2 < (int64_t(1) << 31);
-  auto launch = [&](auto f32, auto bufc) {
-    prefill_chunked_kernel<decltype(f32)::value, decltype(bufc)::value>
-        <<<unsigned(blocks), kThreads, 0, s>>>(wkv_layer, num_rows, H, slot_ids, cu_seqlens,
-                                               seq_order, nseq, in, y, total_tokens, zero_init,
-                                               scale);
-  };
-  using T_ = std::true_type;
-  using F_ = std::false_type;
-  if (y_dtype == WKV7_Y_F32) {
-    if (buf) launch(T_{}, T_{}); else launch(T_{}, F_{});
-  } else {
-    if (buf) launch(F_{}, T_{}); else launch(F_{}, F_{});
-  }
-  return launch_status();
+  const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr};
+  return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
+                        total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,
+                        runs, stream);
+}
+
+extern "C" int wkv7_prefill_runs(float* wkv_layer, int64_t num_rows, int32_t H,
+                                 const int32_t* slot_ids, const int32_t* cu_seqlens,
+                                 const int32_t* seq_order, int32_t nseq, int64_t total_tokens,
+                                 const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                                 const uint16_t* v, const uint16_t* a, const uint16_t* b, void* y,
+                                 int32_t y_dtype, int32_t zero_init, float scale,
+                                 const int32_t* run_flags, const int32_t* cu_alt,
+                                 int32_t n_primary, float* state_alt, int64_t alt_rows,
+                                 void* y_alt, void* stream) {
+  if (nseq < 0 || H < 1 || num_rows < 1 || total_tokens < 0 || alt_rows < 0) return WKV7_ERR_ARG;
+  if (n_primary < 0 || n_primary > nseq) return WKV7_ERR_ARG;
+  if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
+  if (nseq == 0) return WKV7_OK;
+  if (!wkv_layer || !slot_ids || (n_primary > 0 && !cu_seqlens)) return WKV7_ERR_ARG;
+  if (n_primary < nseq && !cu_alt) return WKV7_ERR_ARG;
+  if (alt_rows > 0 && !state_alt) return WKV7_ERR_ARG;
+  if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
+  if (!inputs_aligned(r, w, k, v, a, b)) return WKV7_ERR_SHAPE;
+  const Runs runs{run_flags, cu_alt, n_primary, state_alt, alt_rows, y_alt ? y_alt : y};
+  return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
+                        total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,
+                        runs, stream);
 }

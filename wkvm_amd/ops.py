@@ -273,29 +273,21 @@ def segment_cuts(length: int, segments: int) -> list[int]:
 def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, v, a, b, *,
                           segments: int, zero_init: bool = False, scale: float = 1.0,
                           out: torch.Tensor | None = None,
-                          out_dtype: torch.dtype = torch.bfloat16,
-                          side_stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+                          out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """``wkv7_prefill_varlen`` with each sequence cut into up to ``segments``
     pieces that run side by side, for batches of few, long sequences (one
     sequence of H heads keeps only H compute units busy).
 
-    The scan is linear in its initial state. Two ragged launches run at once
-    (the second on ``side_stream``, a default-priority stream made here if not
-    given), both on the caller's token arrays:
-    * the main runs: segment 0 of each sequence from its slot state (or zero),
-      every later segment g from zero state -> y0_g and final state H0_g;
-    * the transition runs: every later segment from the identity with k = v
-      = 0 -> its transition Phi_g as the final state and q_g = (scale r)^T
-      Phi_t as y.
-    Then, segment by segment with H_in the state entering it (fp32):
-    y_g = y0_g + q_g H_in and H_out = H0_g + Phi_g H_in. Results match the
-    one-pass scan to fp32 rounding; y is rounded to ``out_dtype`` once, after
-    the correction. ``slot_ids`` and ``cu_seqlens`` are host sequences.
-
-    The combination runs as ordinary torch ops (about 0.6 ms of host time per
-    call on the MI355X box), so this pays only for long sequences: one 16,384-
-    token sequence at H = 32 takes 0.78 ms with 4 segments against 1.12 ms in
-    one pass; at 4,096 tokens and below the one-pass kernel is faster."""
+    The scan is linear in its initial state. One ``wkv7_prefill_runs`` launch
+    holds, per sequence, segment 0 from the slot state (or zero) and, for every
+    later segment g, a run from zero state (y0_g, final state H0_g) and a run
+    from the identity with k = v = 0 (its transition Phi_g as the final state,
+    q_g = (scale r)^T Phi_t as y). ``wkv7_segment_chain`` then walks the
+    segments in order (H_out = H0_g + Phi_g H_in, ending in the slot) and
+    ``wkv7_segment_correct`` writes y = y0 + q H_in for every token, in fp32,
+    rounded once to ``out_dtype``. Results match the one-pass scan to fp32
+    rounding. ``slot_ids`` and ``cu_seqlens`` are host sequences; the plan is
+    one upload, the scratch four tensors from the caching allocator."""
     rows, H = _check_pool(wkv_layer)
     dev = wkv_layer.device
     if segments < 1:
@@ -309,84 +301,82 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
     if len(cu) != nseq + 1:
         raise ValueError(f"cu_seqlens has {len(cu)} entries for {nseq} sequences")
     dtype = out.dtype if out is not None else out_dtype
-    _y_code(dtype)
+    code = _y_code(dtype)
     y = _out(out, (T, H, HEAD_SIZE), dtype, dev, "out")
-    if nseq == 0:
+    empty = [ids[s] for s in range(nseq) if cu[s] == cu[s + 1]]
+    if zero_init and empty:
+        slot_zero(wkv_layer, empty, slot_dim=0)
+    if T == 0:
         return y
-    # Main runs tile [0, T) in token order (an empty sequence has none). The
-    # transition runs cover the later segments inside the token window
-    # [w0, w1) that holds them; gaps inside the window (segment 0 of a later
-    # sequence) become runs on spare identity rows whose results are unused.
-    main_rows, main_cu, slot_rows = [], [0], []
-    seqs = []  # (slot, row of segment 0 or None, [[b, e, main row]])
-    n_main = 0
+    L = _lib
+    run_slot, run_flags, prim_cu = [], [], [0]
+    alt_slot, alt_flags, alt_pairs = [], [], []
+    seq_tab, seg_tab, blk = [], [], []
+    n_alt = nsegs = 0
+
+    def blocks(b_, e_, seg):
+        for t in range(b_, e_, 64):
+            blk.extend((t, min(64, e_ - t), seg))
+
     for s in range(nseq):
         beg, end = cu[s], cu[s + 1]
         if beg == end:
-            seqs.append((ids[s], None, []))
             continue
         cuts = segment_cuts(end - beg, segments)
-        row0 = n_main
-        slot_rows.append(ids[s])
-        main_rows.append(row0)
-        main_cu.append(beg + cuts[1])
-        n_main += 1
-        later = []
+        run_slot.append(ids[s])
+        run_flags.append(L.WKV7_RUN_INIT_ZERO if zero_init else 0)
+        prim_cu.append(beg + cuts[1])
+        blocks(beg, beg + cuts[1], -1)
+        first = nsegs
         for g in range(1, len(cuts) - 1):
-            later.append([beg + cuts[g], beg + cuts[g + 1], n_main])
-            main_rows.append(n_main)
-            main_cu.append(beg + cuts[g + 1])
-            n_main += 1
-        seqs.append((ids[s], row0, later))
-    segs = [seg for _, _, later in seqs for seg in later]
-    phi_rows, phi_cu, n_phi = [], [0], 0
-    w0 = segs[0][0] if segs else 0
-    for seg in segs:
-        if phi_cu[-1] < seg[0] - w0:  # a gap: filler run
-            phi_rows.append(n_phi)
-            phi_cu.append(seg[0] - w0)
-            n_phi += 1
-        seg.append(n_phi)  # transition row
-        phi_rows.append(n_phi)
-        phi_cu.append(seg[1] - w0)
-        n_phi += 1
-    w1 = w0 + phi_cu[-1]
-    y32 = torch.empty((T, H, HEAD_SIZE), dtype=torch.float32, device=dev)
-    if n_main:
-        pool = torch.zeros((n_main, H, HEAD_SIZE, HEAD_SIZE), dtype=torch.float32, device=dev)
-        if not zero_init:
-            slot_copy(pool, [row for _, row, _ in seqs if row is not None], wkv_layer, slot_rows,
-                      slot_dim=0)
-        if segs:
-            main = torch.cuda.current_stream(dev)
-            side = side_stream if side_stream is not None else torch.cuda.Stream(dev)
-            phi = torch.eye(HEAD_SIZE, dtype=torch.float32, device=dev).expand(
-                n_phi, H, HEAD_SIZE, HEAD_SIZE).contiguous()
-            zkv = torch.zeros((w1 - w0, H, HEAD_SIZE), dtype=torch.bfloat16, device=dev)
-            q32 = torch.empty((w1 - w0, H, HEAD_SIZE), dtype=torch.float32, device=dev)
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                win = [x[w0:w1] for x in xs]
-                wkv7_prefill_varlen(phi, phi_rows, phi_cu, win[0], win[1], zkv, zkv, win[4],
-                                    win[5], scale=scale, out=q32)
-        wkv7_prefill_varlen(pool, main_rows, main_cu, *xs, scale=scale, out=y32)
-        if segs:
-            main.wait_stream(side)
-            for t in (phi, zkv, q32):
-                t.record_stream(side)
-    # combine in order (fp32)
-    for slot, row0, later in seqs:
-        if row0 is None:
-            if zero_init:
-                wkv_layer[slot].zero_()
-            continue
-        h_in = pool[row0]
-        for b_, e_, row_main, row_phi in later:
-            q = q32[b_ - w0:e_ - w0].transpose(0, 1)  # [H, n, 64]
-            y32[b_:e_] += torch.bmm(q, h_in).transpose(0, 1)
-            h_in = pool[row_main] + torch.bmm(phi[row_phi], h_in)
-        wkv_layer[slot].copy_(h_in)
-    y.copy_(y32)
+            b_, e_ = beg + cuts[g], beg + cuts[g + 1]
+            run_slot.append(n_alt)
+            run_flags.append(L.WKV7_RUN_INIT_ZERO | L.WKV7_RUN_STATE_ALT)
+            prim_cu.append(e_)
+            alt_slot.append(n_alt + 1)
+            alt_flags.append(L.WKV7_RUN_INIT_IDENTITY | L.WKV7_RUN_KV_ZERO | L.WKV7_RUN_Y_ALT
+                             | L.WKV7_RUN_STATE_ALT)
+            alt_pairs += [b_, e_]
+            seg_tab += [n_alt, n_alt + 1]
+            blocks(b_, e_, nsegs)
+            n_alt += 2
+            nsegs += 1
+        if nsegs > first:
+            seq_tab += [ids[s], first, nsegs - first]
+    n_primary = len(run_slot)
+    nruns = n_primary + len(alt_slot)
+    lens = [prim_cu[i + 1] - prim_cu[i] for i in range(n_primary)]
+    lens += [alt_pairs[2 * i + 1] - alt_pairs[2 * i] for i in range(len(alt_slot))]
+    order = sorted(range(nruns), key=lambda i: -lens[i])
+    parts = [run_slot + alt_slot, run_flags + alt_flags, prim_cu, alt_pairs or [0, 0], order,
+             seq_tab or [0, 0, 0], seg_tab or [0, 0], blk]
+    plan = torch.tensor([x for p in parts for x in p], dtype=torch.int32, device=dev)
+    views, at = [], 0
+    for p in parts:
+        views.append(plan[at:at + len(p)])
+        at += len(p)
+    v_ids, v_flags, v_cu, v_pairs, v_order, v_seq, v_seg, v_blk = views
+    y0 = torch.empty((T, H, HEAD_SIZE), dtype=torch.float32, device=dev)
+    q = torch.empty_like(y0) if nsegs else y0
+    alt = torch.empty((max(n_alt, 1), H, HEAD_SIZE, HEAD_SIZE), dtype=torch.float32, device=dev)
+    hin = torch.empty((max(nsegs, 1), H, HEAD_SIZE, HEAD_SIZE), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    stream = _stream_ptr(dev)
+    rc = lib.wkv7_prefill_runs(wkv_layer.data_ptr(), rows, H, v_ids.data_ptr(), v_cu.data_ptr(),
+                               v_order.data_ptr(), nruns, T, *[x.data_ptr() for x in xs],
+                               y0.data_ptr(), _lib.WKV7_Y_F32, 0, float(scale),
+                               v_flags.data_ptr(), v_pairs.data_ptr(), n_primary,
+                               alt.data_ptr(), n_alt, q.data_ptr(), stream)
+    _lib.check(rc, "wkv7_prefill_runs")
+    if nsegs:
+        rc = lib.wkv7_segment_chain(wkv_layer.data_ptr(), rows, H, alt.data_ptr(), n_alt,
+                                    v_seq.data_ptr(), len(seq_tab) // 3, v_seg.data_ptr(), nsegs,
+                                    hin.data_ptr(), stream)
+        _lib.check(rc, "wkv7_segment_chain")
+    rc = lib.wkv7_segment_correct(T, H, y0.data_ptr(), q.data_ptr(), v_blk.data_ptr(),
+                                  len(blk) // 3, hin.data_ptr(), nsegs, y.data_ptr(), code,
+                                  stream)
+    _lib.check(rc, "wkv7_segment_correct")
     return y
 
 

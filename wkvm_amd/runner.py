@@ -33,11 +33,23 @@ LayerInputs = Sequence[torch.Tensor]  # (r, w, k, v, a, b)
 
 
 class WKV7Runner:
-    def __init__(self, bank: RWKV7StateBank, prefill_chunk: int = 512) -> None:
+    # Chunks at least this long run segmented when ``prefill_segments`` is set
+    # (the segmented form is faster from about 2k tokens of one sequence).
+    SEGMENT_MIN_TOKENS = 2048
+
+    def __init__(self, bank: RWKV7StateBank, prefill_chunk: int = 512,
+                 prefill_segments: int | None = None) -> None:
+        """``prefill_segments``: cut each prefill chunk of at least
+        ``SEGMENT_MIN_TOKENS`` tokens into that many segments that run side by
+        side (``ops.wkv7_prefill_segments``); ``None`` runs every chunk in one
+        pass. Results agree to fp32 rounding."""
         if prefill_chunk < 1:
             raise ValueError("prefill_chunk must be >= 1")
+        if prefill_segments is not None and prefill_segments < 1:
+            raise ValueError("prefill_segments must be >= 1")
         self.bank = bank
         self.prefill_chunk = prefill_chunk
+        self.prefill_segments = prefill_segments
         self.device = bank.device
 
     def _check_layers(self, layer_inputs: Sequence[LayerInputs]) -> None:
@@ -66,9 +78,16 @@ class WKV7Runner:
             if n not in plans:
                 plans[n] = torch.tensor([0, n, 0], dtype=torch.int32, device=self.device)
             plan = plans[n]
+            segmented = (self.prefill_segments or 1) > 1 and n >= self.SEGMENT_MIN_TOKENS
             for layer, xs in enumerate(layer_inputs):
-                self.bank.prefill_wkv(layer, ids, plan[:2], *(x[start:start + n] for x in xs),
-                                      out=ys[layer][start:start + n], seq_order=plan[2:])
+                chunk = [x[start:start + n] for x in xs]
+                if segmented:
+                    ops.wkv7_prefill_segments(self.bank.wkv[layer], [slots["wkv"]], [0, n],
+                                              *chunk, segments=self.prefill_segments,
+                                              out=ys[layer][start:start + n])
+                else:
+                    self.bank.prefill_wkv(layer, ids, plan[:2], *chunk,
+                                          out=ys[layer][start:start + n], seq_order=plan[2:])
         return ys
 
     @torch.inference_mode()
