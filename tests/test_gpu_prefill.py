@@ -388,12 +388,33 @@ def test_runner_segmented_prefill_matches_one_pass(dev):
     inputs = [synthetic.order(synthetic.wkv7_vectors((T, 4, 64), gen, device=dev))
               for _ in range(2)]
     outs, finals = [], []
-    for segs in (None, 4):
+    for segs in (None, 4, "auto"):
         bank = RWKV7StateBank(lay, num_slots=3, device=dev)
         bank.wkv[:, 2].normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(68))
         run = WKV7Runner(bank, prefill_chunk=2048, prefill_segments=segs)
         ys = run.prefill(inputs, {"wkv": 2, "shift": 2}, out_dtype=torch.float32)
         outs.append(torch.stack(ys))
         finals.append(bank.wkv[:, 2].clone())
-    assert U.rel_l2(U.f64(outs[1]), U.f64(outs[0])) <= 1e-5
-    assert U.rel_l2(U.f64(finals[1]), U.f64(finals[0])) <= 1e-5
+    for i in (1, 2):
+        assert U.rel_l2(U.f64(outs[i]), U.f64(outs[0])) <= 1e-5
+        assert U.rel_l2(U.f64(finals[i]), U.f64(finals[0])) <= 1e-5
+
+
+def test_fla_signature_long_single_sequence_runs_segmented(dev):
+    """chunk_rwkv7 with one long sequence picks the segmented form (few busy
+    compute units) and still matches the oracle, from an initial state and
+    from zero."""
+    B, T, H = 1, 2100, 4
+    assert ops.auto_segments(H, [T], dev) > 1 and ops.auto_segments(H, [500], dev) == 1
+    gen = synthetic.make_generator(71)
+    vecs = synthetic.wkv7_vectors((B, T, H, 64), gen)
+    h0 = synthetic.initial_states((B, H, 64, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    bits = [U.bits(vecs[n][0]) for n in "rwkvab"]
+    for init in (h0, None):
+        o, hT = ops.chunk_rwkv7(*xs, scale=1.0, initial_state=None if init is None else init.to(dev))
+        y_ref, h_ref = O.scan_bf16(np.array([0, T]), *bits,
+                                   pool=None if init is None else init.numpy(),
+                                   slot_ids=None if init is None else [0])
+        assert U.rel_l2(U.f64(hT), h_ref) <= REL_L2
+        assert U.rel_l2(U.f64(o[0]), O.round_f64_to_bf16(y_ref)) <= REL_L2

@@ -182,6 +182,10 @@ def test_runner_argument_errors():
 
     with pytest.raises(ValueError):
         WKV7Runner(FakeBank(), prefill_chunk=0)
+    for bad in (0, "four", 2.0):
+        with pytest.raises(ValueError, match="prefill_segments"):
+            WKV7Runner(FakeBank(), prefill_segments=bad)
+    WKV7Runner(FakeBank(), prefill_segments="auto")
     run = WKV7Runner(FakeBank(), prefill_chunk=64)
     empty = tuple(torch.zeros((0, 2, 64), dtype=torch.bfloat16) for _ in range(6))
     with pytest.raises(ValueError, match="empty prompt"):

@@ -705,6 +705,21 @@ def time_mix_output(H: int, y, r, k, v, g, r_k, ln_w, ln_b, eps: float,
 
 # -- fla wkv-op signatures --------------------------------------------------------------
 
+def auto_segments(H: int, lens: Sequence[int], device: torch.device) -> int:
+    """Segments per sequence for ``wkv7_prefill_segments`` when a one-pass
+    launch would leave most compute units idle: the busy (sequence, head)
+    workgroups fill at most a quarter of the GPU and the longest sequence has
+    at least 2,048 tokens (below that the split does not pay). G segments
+    take 2G - 1 workgroups per (sequence, head)."""
+    busy = sum(1 for n in lens if n > 0) * H
+    if busy == 0 or max(lens) < 2048:
+        return 1
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    if 4 * busy > cus:
+        return 1
+    return max(1, min(4, (cus // busy + 1) // 2))
+
+
 def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens, head_first):
     if head_first:
         r, w, k, v, a, b = (x.transpose(1, 2) for x in (r, w, k, v, a, b))
@@ -733,9 +748,16 @@ def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqle
         pool = initial_state.to(device=dev, dtype=torch.float32).clone().contiguous()
     else:
         pool = torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
-    ids = torch.arange(nseq, dtype=torch.int32, device=dev)
-    y = wkv7_prefill_varlen(pool, ids, cu, *flat, zero_init=initial_state is None, scale=scale,
-                            out_dtype=r.dtype)
+    host_cu = cu.tolist() if isinstance(cu, torch.Tensor) else [int(c) for c in cu]
+    G = auto_segments(H, [host_cu[i + 1] - host_cu[i] for i in range(nseq)], dev)
+    if G > 1:  # few long sequences: run their segments side by side
+        y = wkv7_prefill_segments(pool, list(range(nseq)), host_cu, *flat, segments=G,
+                                  zero_init=initial_state is None, scale=scale,
+                                  out_dtype=r.dtype)
+    else:
+        ids = torch.arange(nseq, dtype=torch.int32, device=dev)
+        y = wkv7_prefill_varlen(pool, ids, cu, *flat, zero_init=initial_state is None,
+                                scale=scale, out_dtype=r.dtype)
     o = y.reshape(B, T, H, K)
     if head_first:
         o = o.transpose(1, 2)
@@ -758,7 +780,9 @@ def fused_recurrent_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=No
 def chunk_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=None,
                 output_final_state: bool = True, cu_seqlens=None, head_first: bool = False):
     """fla-signature chunked WKV7 (the reference's prefill path, T >= 64).
-    Same arguments and results as ``fused_recurrent_rwkv7``."""
+    Same arguments and results as ``fused_recurrent_rwkv7``. Few long
+    sequences (``auto_segments``) run segmented, to fp32 rounding of the
+    one-pass result."""
     return _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
                    head_first)
 

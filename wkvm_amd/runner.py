@@ -38,15 +38,17 @@ class WKV7Runner:
     SEGMENT_MIN_TOKENS = 2048
 
     def __init__(self, bank: RWKV7StateBank, prefill_chunk: int = 512,
-                 prefill_segments: int | None = None) -> None:
+                 prefill_segments: int | str | None = None) -> None:
         """``prefill_segments``: cut each prefill chunk of at least
         ``SEGMENT_MIN_TOKENS`` tokens into that many segments that run side by
-        side (``ops.wkv7_prefill_segments``); ``None`` runs every chunk in one
-        pass. Results agree to fp32 rounding."""
+        side (``ops.wkv7_prefill_segments``); ``"auto"`` picks the count from
+        the compute units one chunk leaves idle (``ops.auto_segments``);
+        ``None`` runs every chunk in one pass. Results agree to fp32 rounding."""
         if prefill_chunk < 1:
             raise ValueError("prefill_chunk must be >= 1")
-        if prefill_segments is not None and prefill_segments < 1:
-            raise ValueError("prefill_segments must be >= 1")
+        if prefill_segments is not None and prefill_segments != "auto" and (
+                not isinstance(prefill_segments, int) or prefill_segments < 1):
+            raise ValueError("prefill_segments must be >= 1, 'auto' or None")
         self.bank = bank
         self.prefill_chunk = prefill_chunk
         self.prefill_segments = prefill_segments
@@ -78,17 +80,24 @@ class WKV7Runner:
             if n not in plans:
                 plans[n] = torch.tensor([0, n, 0], dtype=torch.int32, device=self.device)
             plan = plans[n]
-            segmented = (self.prefill_segments or 1) > 1 and n >= self.SEGMENT_MIN_TOKENS
+            G = self._segments(n, H)
             for layer, xs in enumerate(layer_inputs):
                 chunk = [x[start:start + n] for x in xs]
-                if segmented:
+                if G > 1:
                     ops.wkv7_prefill_segments(self.bank.wkv[layer], [slots["wkv"]], [0, n],
-                                              *chunk, segments=self.prefill_segments,
+                                              *chunk, segments=G,
                                               out=ys[layer][start:start + n])
                 else:
                     self.bank.prefill_wkv(layer, ids, plan[:2], *chunk,
                                           out=ys[layer][start:start + n], seq_order=plan[2:])
         return ys
+
+    def _segments(self, n: int, H: int) -> int:
+        if self.prefill_segments is None or n < self.SEGMENT_MIN_TOKENS:
+            return 1
+        if self.prefill_segments == "auto":
+            return ops.auto_segments(H, [n], self.device)
+        return self.prefill_segments
 
     @torch.inference_mode()
     def decode_step(self, slot_batch: list[dict[str, int]],
