@@ -663,11 +663,23 @@ def bench_time_mix(torch, dev, args):
 
     eager_us = timed(eager_step, iters=5)
     graph_us = timed(tg.replay, iters=10)
+    # the same step with the projections on the vendor BLAS (two side streams)
+    saved = RWKV7TimeMix.PROJ_MAX_ROWS
+    RWKV7TimeMix.PROJ_MAX_ROWS = 0
+    try:
+        tg_blas = TimeMixDecodeGraph(bank, layers, 256, side_streams=2)
+    finally:
+        RWKV7TimeMix.PROJ_MAX_ROWS = saved
+    tg_blas.set_slots(dslots)
+    tg_blas.x.copy_(tg.x)
+    blas_us = timed(tg_blas.replay, iters=10)
     res["decode_step_24_layers"] = {"eager_us": eager_us, "graph_us": graph_us,
-                                    "slot_steps_per_s_graph": 256 / (graph_us * 1e-6)}
+                                    "slot_steps_per_s_graph": 256 / (graph_us * 1e-6),
+                                    "graph_us_vendor_blas": blas_us}
     log(f"time-mix decode step, 24 layers x 256 slots: eager {eager_us:.0f} us, graph "
-        f"{graph_us:.0f} us ({256 / (graph_us * 1e-6):.0f} slot-steps/s)")
-    del bank, tg, layers
+        f"{graph_us:.0f} us ({256 / (graph_us * 1e-6):.0f} slot-steps/s); projections on "
+        f"the vendor BLAS: graph {blas_us:.0f} us")
+    del bank, tg, tg_blas, layers
     torch.cuda.empty_cache()
     return res
 

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 5
+#define WKV7_ABI_VERSION 6
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -338,6 +338,49 @@ int wkv7_time_mix_output(int64_t total_tokens, int32_t H, const void *y, int32_t
                          const uint16_t *r, const uint16_t *k, const uint16_t *v,
                          const uint16_t *g, const uint16_t *r_k, const uint16_t *ln_w,
                          const uint16_t *ln_b, float eps, uint16_t *out, void *stream);
+
+/*
+ * Grouped projection GEMMs of the RWKV-7 time-mix block, for few rows (decode
+ * batches): up to WKV7_PROJ_MAX_GROUPS independent products in one launch,
+ *     y_g[m][c] = act_g( sum_j x_g[m][j] w_g[c][j] + bias_g[c] ),
+ * bf16 operands on the matrix cores, fp32 accumulation, bias and activation
+ * on the fp32 sum, one bf16 rounding per output. All groups share the row
+ * count m; each has its own k, n, pointers and strides.
+ *
+ * Replaces the nn.Linear calls of fla's RWKV7Attention (external; reached
+ * through the model forward, wkvm/runner/runner.py:80-88): the r, k, v and o
+ * projections (weights [out, in] as nn.Linear holds them) and both stages of
+ * the w, a, v and g LoRAs, with the LoRAs' inner tanh and sigmoid fused into
+ * the first stage's epilogue.
+ *
+ *   x     [m, k] bf16, row stride ldx elements (ldx >= k, ldx % 8 == 0)
+ *   w     [n, k] bf16, row stride ldw elements (ldw >= k, ldw % 8 == 0)
+ *   bias  [n] bf16, or NULL
+ *   y     [m, n] bf16, row stride ldy elements (ldy >= n)
+ * k must be a positive multiple of 32; x and w 16-byte aligned (else
+ * WKV7_ERR_SHAPE). y must not overlap any group's x, w or bias.
+ */
+#define WKV7_PROJ_MAX_GROUPS 8
+#define WKV7_ACT_NONE 0
+#define WKV7_ACT_TANH 1
+#define WKV7_ACT_SIGMOID 2
+
+typedef struct wkv7_proj_group {
+  const uint16_t *x;
+  const uint16_t *w;
+  const uint16_t *bias;
+  uint16_t *y;
+  int64_t ldx;
+  int64_t ldw;
+  int64_t ldy;
+  int32_t n;
+  int32_t k;
+  int32_t act;
+  int32_t reserved; /* set to 0 */
+} wkv7_proj_group;
+
+int wkv7_proj_grouped(int64_t m, const wkv7_proj_group *groups, int32_t ngroups,
+                      void *stream);
 
 #ifdef __cplusplus
 }

@@ -265,9 +265,11 @@ def test_time_mix_decode_graph_replays_match_eager(dev):
         del scratch
 
 
-def test_block_side_streams_give_the_same_bytes(dev):
+def test_block_side_streams_give_the_same_bytes(dev, monkeypatch):
     """The block's independent GEMM chains on side streams (eager) produce the
-    same outputs and state as the single-stream block."""
+    same outputs and state as the single-stream block (vendor-BLAS path, as
+    taken above PROJ_MAX_ROWS tokens)."""
+    monkeypatch.setattr(RWKV7TimeMix, "PROJ_MAX_ROWS", 0)
     layout = RWKV7StateLayout(n_layer=2, hidden_size=256, num_heads=4, head_dim=64,
                               head_v_dim=64, dtype=torch.bfloat16)
     banks = [RWKV7StateBank(layout, 12, device=dev) for _ in range(2)]
@@ -290,3 +292,35 @@ def test_block_side_streams_give_the_same_bytes(dev):
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(banks[0].wkv, banks[1].wkv) and torch.equal(banks[0].shift, banks[1].shift)
+
+
+def test_block_grouped_projections_match_vendor_path(dev, monkeypatch):
+    """The block with its projections on wkv7_proj_grouped (decode-sized
+    batches) against the same block on the vendor BLAS: both round every
+    GEMM output to bf16 once (the grouped path applies the LoRA tanh/sigmoid
+    before that rounding), so outputs and state agree to bf16 rounding."""
+    layout = RWKV7StateLayout(n_layer=3, hidden_size=512, num_heads=8, head_dim=64,
+                              head_v_dim=64, dtype=torch.bfloat16)
+    banks = [RWKV7StateBank(layout, 40, device=dev) for _ in range(2)]
+    banks[0].wkv.normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(105))
+    banks[0].shift.copy_(_bf(banks[0].shift.shape, dev, 106))
+    banks[1].wkv.copy_(banks[0].wkv)
+    banks[1].shift.copy_(banks[0].shift)
+    layers = [RWKV7TimeMix.random(layout, l, dev, seed=9) for l in range(3)]
+    slots = list(range(3, 35))
+    x = _bf((3, len(slots), 512), dev, 107)
+    outs = []
+    for bank, rows in zip(banks, (RWKV7TimeMix.PROJ_MAX_ROWS, 0)):
+        monkeypatch.setattr(RWKV7TimeMix, "PROJ_MAX_ROWS", rows)
+        batch = TokenBatch.plan(bank, slots)
+        v_first, o = None, []
+        for l, layer in enumerate(layers):
+            y, v_first = layer.forward(bank, x[l], batch, v_first)
+            o.append(y)
+        outs.append(torch.stack(o))
+    torch.cuda.synchronize()
+    assert torch.equal(banks[0].shift, banks[1].shift)
+    err = U.normwise_max(U.f64(banks[0].wkv), U.f64(banks[1].wkv))
+    rel = U.rel_l2(U.f64(outs[0]), U.f64(outs[1]))
+    print(f"grouped vs vendor: state {err:.2e}, outputs rel-L2 {rel:.2e}")
+    assert err <= 1e-2 and rel <= 1e-2

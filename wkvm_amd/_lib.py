@@ -29,12 +29,25 @@ WKV7_RUN_Y_ALT = 8
 WKV7_RUN_STATE_ALT = 16
 WKV7_TO_HOST = 0
 WKV7_FROM_HOST = 1
+WKV7_PROJ_MAX_GROUPS = 8
+WKV7_ACT_NONE = 0
+WKV7_ACT_TANH = 1
+WKV7_ACT_SIGMOID = 2
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
+
+
+
+class ProjGroup(ctypes.Structure):
+    """struct wkv7_proj_group of include/wkv7.h."""
+    _fields_ = [("x", _vp), ("w", _vp), ("bias", _vp), ("y", _vp), ("ldx", _i64),
+                ("ldw", _i64), ("ldy", _i64), ("n", _i32), ("k", _i32), ("act", _i32),
+                ("reserved", _i32)]
+
 
 # name -> (restype, argtypes); must match include/wkv7.h.
 SIGNATURES = {
@@ -64,6 +77,7 @@ SIGNATURES = {
         _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "wkv7_time_mix_output": (ctypes.c_int, [
         _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
+    "wkv7_proj_grouped": (ctypes.c_int, [_i64, ctypes.POINTER(ProjGroup), _i32, _vp]),
 }
 
 _lib = None

@@ -703,6 +703,72 @@ def time_mix_output(H: int, y, r, k, v, g, r_k, ln_w, ln_b, eps: float,
     return o
 
 
+ACTIVATIONS = {None: _lib.WKV7_ACT_NONE, "tanh": _lib.WKV7_ACT_TANH,
+               "sigmoid": _lib.WKV7_ACT_SIGMOID}
+
+
+def proj_grouped(products: Sequence[tuple], outs: Sequence[torch.Tensor | None] | None = None,
+                 ) -> list[torch.Tensor]:
+    """Independent projections ``act(x @ w.T + bias)`` in one launch
+    (``wkv7_proj_grouped``): ``products`` holds up to 8 tuples ``(x, w)``,
+    ``(x, w, bias)`` or ``(x, w, bias, act)`` with ``x [M, k]`` (row stride
+    a multiple of 8, unit column stride), ``w [n, k]`` bf16 (nn.Linear's
+    [out, in]), ``bias [n]`` or None and ``act`` None, ``"tanh"`` or
+    ``"sigmoid"``; every ``x`` has the same M. Returns the ``[M, n]`` bf16
+    outputs (written into ``outs[i]`` where given, which may be strided
+    row views)."""
+    if not 1 <= len(products) <= _lib.WKV7_PROJ_MAX_GROUPS:
+        raise ValueError(f"1..{_lib.WKV7_PROJ_MAX_GROUPS} products per launch, got {len(products)}")
+    groups = (_lib.ProjGroup * len(products))()
+    ys, keep = [], []
+    M = None
+    for i, prod in enumerate(products):
+        x, w = prod[0], prod[1]
+        bias = prod[2] if len(prod) > 2 else None
+        act = prod[3] if len(prod) > 3 else None
+        if act not in ACTIVATIONS:
+            raise ValueError(f"act must be one of {list(ACTIVATIONS)}, got {act!r}")
+        for t, n in ((x, "x"), (w, "w")):
+            _require_cuda(t, n)
+            if t.dtype != torch.bfloat16 or t.dim() != 2:
+                raise ValueError(f"{n} must be a 2-D bfloat16 tensor")
+        if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+            x = x.clone(memory_format=torch.contiguous_format)
+        w = _bf16_2d(w, "w")
+        m, k = int(x.shape[0]), int(x.shape[1])
+        n = int(w.shape[0])
+        if M is None:
+            M = m
+        if m != M:
+            raise ValueError("every product needs the same row count")
+        if int(w.shape[1]) != k:
+            raise ValueError(f"w must be [n, {k}], got {tuple(w.shape)}")
+        if k < 32 or k % 32:
+            raise ValueError(f"k must be a positive multiple of 32, got {k}")
+        if bias is not None:
+            bias = _bf16_2d(bias.reshape(-1), "bias", (n,))
+        y = outs[i] if outs is not None and i < len(outs) else None
+        if y is None:
+            y = torch.empty((M, n), dtype=torch.bfloat16, device=x.device)
+        else:
+            _require_cuda(y, "out")
+            if y.dtype != torch.bfloat16 or tuple(y.shape) != (M, n) or y.stride(1) != 1:
+                raise ValueError(f"out must be a bf16 [{M}, {n}] tensor with unit column stride")
+        for t in (w, y) + ((bias,) if bias is not None else ()):
+            if t.device != x.device:
+                raise ValueError("projection tensors must share a device")
+        groups[i] = _lib.ProjGroup(x.data_ptr(), w.data_ptr(), _ptr(bias), y.data_ptr(),
+                                   x.stride(0), w.stride(0), y.stride(0), n, k,
+                                   ACTIVATIONS[act], 0)
+        keep += [x, w, bias]
+        ys.append(y)
+    if M:
+        rc = _lib.load().wkv7_proj_grouped(M, groups, len(products),
+                                           _stream_ptr(ys[0].device))
+        _lib.check(rc, "wkv7_proj_grouped")
+    return ys
+
+
 # -- fla wkv-op signatures --------------------------------------------------------------
 
 def auto_segments(H: int, lens: Sequence[int], device: torch.device) -> int:

@@ -10,19 +10,25 @@ place, and every element-wise stage is one of this library's kernels:
     -> token_shift_mix      bank.shift[l, 0] (conv_state) read and updated
                             in place; the six lerp mixes xr..xg
     -> projections          r, k, v, o [D, D] and the LoRAs (w: tanh, a, v:
-                            linear, g: sigmoid inside) -- plain GEMMs on the
-                            vendor BLAS through torch's linear
+                            linear, g: sigmoid inside): for up to
+                            PROJ_MAX_ROWS tokens two grouped launches of
+                            wkv7_proj_grouped (all first stages, then all
+                            second stages with their biases) and one for o;
+                            above that the vendor BLAS through torch's linear
     -> time_mix_inputs      log-decay w, k, v (v_first lerp), a = -kk, b = kk*a
     -> WKV7                 wkv7_decode_slots (one token per slot) or
                             wkv7_prefill_varlen (ragged), bank.wkv[l] in place
     -> time_mix_output      per-head GroupNorm, bonus, gate
     -> o_proj
 
-The LoRA inner activations act on the small [T, rank] tensors between two
-GEMMs and stay in torch. Weights are stored [out, in] as nn.Linear holds
-them (each projection is ``linear(x, W)``); the vendor BLAS is tuned for that
-layout (a 256 x 2048 x 2048 projection: 9.6 us against 12.5 us for [in, out]
-weights, inside a HIP graph on the MI355X). Parameter names follow fla's
+Weights are stored [out, in] as nn.Linear holds them (each projection is
+``linear(x, W)``), the layout both the grouped kernel and the vendor BLAS
+read best. At decode sizes each library GEMM is a separate 4-13 us launch;
+the grouped kernel runs the seven first-stage products of a 256-token
+batch in ~23 us and the four second stages in ~6 us (MI355X, inside a HIP
+graph), with the LoRA activations fused into the first stage. Large token
+counts (prefill) stay on the vendor BLAS, which reaches ~55 % of the bf16
+matrix peak there. Parameter names follow fla's
 RWKV7Attention (x_r .. x_g, k_k, k_a, r_k, w0/w1/w2, a0/a1/a2, v0/v1/v2,
 g1/g2, g_norm). The GroupNorm epsilon is head_dim * 1e-5.
 """
@@ -87,6 +93,9 @@ class RWKV7TimeMix:
     likewise ``a*``, ``v*`` (layers after the first), ``g1`` [rg, D], ``g2``
     [D, rg], and ``k_k``, ``k_a``, ``r_k``, ``ln_w``, ``ln_b`` [D]."""
 
+    # Token counts up to this run their projections through wkv7_proj_grouped.
+    PROJ_MAX_ROWS = 512
+
     def __init__(self, layout: RWKV7StateLayout, layer_idx: int,
                  weights: dict[str, torch.Tensor]) -> None:
         self.layout = layout
@@ -137,17 +146,20 @@ class RWKV7TimeMix:
         row ``bank.shift[l, 0]`` and wkv state ``bank.wkv[l]`` advance in
         place. ``zero_init`` starts prefill sequences from zero wkv state.
 
-        ``streams`` (side streams of default priority): the projection and
-        LoRA chains are independent of one another, so they are forked onto
-        these streams after the token shift and joined before the WKV inputs.
-        At decode batch sizes each of these GEMMs fills only part of the GPU,
-        and running them side by side shortens the block; the results are the
-        same bytes either way."""
+        ``streams`` (side streams of default priority; used above
+        ``PROJ_MAX_ROWS`` tokens, where the projections run on the vendor
+        BLAS): the projection and LoRA chains are independent of one
+        another, so they are forked onto these streams after the token shift
+        and joined before the WKV inputs; the results are the same bytes
+        either way."""
         W, l, H = self.w, self.layer_idx, self.layout.num_heads
         if l > 0 and v_first is None:
             raise ValueError("layers after the first need v_first")
         xr, xw, xk, xv, xa, xg = ops.token_shift_mix(x, bank.shift[l, 0], batch.slot_ids,
                                                      W["mix"], batch.cu_seqlens)
+        if batch.tokens <= self.PROJ_MAX_ROWS:
+            return self._forward_grouped(bank, batch, v_first, zero_init,
+                                         (xr, xw, xk, xv, xa, xg))
 
         # the independent chains between the token shift and the WKV inputs
         chains = {
@@ -179,7 +191,34 @@ class RWKV7TimeMix:
             for name, fn in chains.items():
                 res[name] = fn()
         r, k, v, w_l, a_l, g = (res[n] for n in ("r", "k", "v", "w_l", "a_l", "g"))
-        v_l = res.get("v_l")
+        o_in, v_first = self._wkv_stage(bank, batch, v_first, zero_init, r, k, v, w_l, a_l,
+                                        res.get("v_l"), g)
+        return F.linear(o_in, W["o"]), v_first
+
+    def _forward_grouped(self, bank, batch, v_first, zero_init, mixes):
+        """The block with its projections on wkv7_proj_grouped: one launch
+        for the seven first-stage products (r, k, v and the LoRA
+        down-projections, tanh / sigmoid fused), one for the four LoRA
+        up-projections with their biases, one for o."""
+        W, l = self.w, self.layer_idx
+        xr, xw, xk, xv, xa, xg = mixes
+        first = [(xr, W["r"]), (xk, W["k"]), (xv, W["v"]), (xw, W["w1"], None, "tanh"),
+                 (xa, W["a1"]), (xg, W["g1"], None, "sigmoid")]
+        if l > 0:
+            first.append((xv, W["v1"]))
+        r, k, v, hw, ha, hg, *hv = ops.proj_grouped(first)
+        second = [(hw, W["w2"], W["w0"]), (ha, W["a2"], W["a0"]), (hg, W["g2"])]
+        if l > 0:
+            second.append((hv[0], W["v2"], W["v0"]))
+        w_l, a_l, g, *v_l = ops.proj_grouped(second)
+        o_in, v_first = self._wkv_stage(bank, batch, v_first, zero_init, r, k, v, w_l, a_l,
+                                        v_l[0] if v_l else None, g)
+        return ops.proj_grouped([(o_in, W["o"])])[0], v_first
+
+    def _wkv_stage(self, bank, batch, v_first, zero_init, r, k, v, w_l, a_l, v_l, g):
+        """time_mix_inputs -> in-place WKV7 -> time_mix_output; returns the
+        output projection's input and v_first."""
+        W, l, H = self.w, self.layer_idx, self.layout.num_heads
         w, k2, v2, a, b = ops.time_mix_inputs(H, k, v, w_l, a_l, W["k_k"], W["k_a"], v_l,
                                               v_first if l > 0 else None)
         if l == 0:
@@ -192,7 +231,7 @@ class RWKV7TimeMix:
             y = ops.wkv7_prefill_varlen(bank.wkv[l], batch.slot_ids, batch.cu_seqlens, *vec,
                                         zero_init=zero_init, seq_order=batch.order)
         o_in = ops.time_mix_output(H, y, r, k2, v2, g, W["r_k"], W["ln_w"], W["ln_b"], self.eps)
-        return F.linear(o_in, W["o"]), v_first
+        return o_in, v_first
 
 
 class TimeMixDecodeGraph:
@@ -210,7 +249,7 @@ class TimeMixDecodeGraph:
     experiments/m2_engine_bench.py:44-131)."""
 
     def __init__(self, bank: RWKV7StateBank, layers: list[RWKV7TimeMix], batch_size: int,
-                 side_streams: int = 2):
+                 side_streams: int | None = None):
         if batch_size < 1:
             raise ValueError("batch_size must be >= 1")
         if len(layers) < 1 or any(l.layer_idx != i for i, l in enumerate(layers)):
@@ -225,7 +264,11 @@ class TimeMixDecodeGraph:
         self.o: list[torch.Tensor] = []
         batch = TokenBatch(self.plan[:B], self.plan[2 * B:], self.plan[B:2 * B], B, B, True)
         # side streams (default priority) for the block's independent GEMM
-        # chains; the graph keeps their fork/join as parallel branches
+        # chains when they run on the vendor BLAS (batches above
+        # PROJ_MAX_ROWS; default 2 there, none below); the graph keeps their
+        # fork/join as parallel branches
+        if side_streams is None:
+            side_streams = 2 if batch_size > RWKV7TimeMix.PROJ_MAX_ROWS else 0
         self.streams = [torch.cuda.Stream(dev) for _ in range(side_streams)]
         # initialise the BLAS handles and workspaces of every stream before
         # capture (GEMMs only: the bank is not touched until the first replay)
