@@ -8,7 +8,7 @@
 // the workgroups of all groups form one grid, each computing a BM x BN output
 // tile over the whole k.
 //
-// Workgroup: 4 waves in a 2 x 2 grid, each wave a (BM/2) x (BN/2) block of
+// Workgroup: GM x GN waves (4 or 8), each a (BM/GM) x (BN/GN) block of
 // 16 x 16 accumulator tiles on v_mfma_f32_16x16x32_bf16. Operand layout of
 // that instruction (lane l, li = l % 16, lg = l / 16): A lane holds
 // A[li][8lg .. 8lg+7] of a 32-wide k block, B lane holds B[8lg .. 8lg+7][li],
@@ -17,11 +17,13 @@
 // k advances 64 per stage through a ring of S LDS stages whose 128-byte rows
 // hold 8 chunks, chunk c of row r at slot c ^ (r & 7), so the 16 rows a
 // fragment read touches spread over the banks. Stages are filled by direct
-// global -> LDS loads (no register staging) issued S - 1 stages ahead, which
-// keeps ~3 x (BM + BN) x 128 bytes in flight per workgroup: at these sizes the
-// products are bound by memory latency, not by the matrix cores. One barrier
-// per stage. Rows past m and columns past n load a clamped (valid) row and
-// are not stored.
+// global -> LDS loads (no register staging) issued S - 1 stages ahead and
+// spread between the MFMAs of the stage being multiplied. One barrier per
+// stage. Rows past m and columns past n load a clamped (valid) row and are
+// not stored. Tiles are dealt to the XCDs in contiguous runs so that each
+// XCD's L2 keeps the x rows it re-reads.
+#include <type_traits>
+
 #include "wkv7_common.h"
 
 namespace wkv7 {
@@ -30,8 +32,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kProjThreads = 256;
 constexpr int kChunks = 8;  // 16-byte chunks per 64-wide k stage of a row
+
+constexpr int kXcds = 8;  // MI355X: workgroups are dealt round-robin over 8 XCDs
 
 struct ProjArgs {
   wkv7_proj_group g[WKV7_PROJ_MAX_GROUPS];
@@ -39,6 +42,7 @@ struct ProjArgs {
   int64_t m;
   int32_t tiles_m;
   int32_t ngroups;
+  int32_t xcd_span;  // tiles per XCD: ceil(tiles / kXcds)
 };
 
 __device__ __forceinline__ f32x4 mma(const uint4& a, const uint4& b, f32x4 c) {
@@ -100,18 +104,23 @@ __device__ __forceinline__ void wait_pending(int pending) {
   }
 }
 
-template <int BM, int BN, int S>
-__global__ __launch_bounds__(kProjThreads) void proj_kernel(const ProjArgs args) {
-  constexpr int WM = BM / 2, WN = BN / 2;     // wave tile
+template <int BM, int BN, int S, int GM, int GN>
+__global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args) {
+  constexpr int NW = GM * GN;                 // waves, a GM x GN grid
+  constexpr int WM = BM / GM, WN = BN / GN;   // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;   // accumulator tiles per wave
   // Each wave-wide direct load fills 1 KiB of a stage = 8 rows; a thread
   // issues L of them per stage.
   constexpr int kRowsPerLoad = 8;
-  constexpr int L = (BM + BN) / (kRowsPerLoad * 4);
-  static_assert(TM >= 1 && TN >= 1 && (BM + BN) % 32 == 0 && BM % 8 == 0, "tile shape");
+  constexpr int L = (BM + BN) / (kRowsPerLoad * NW);
+  static_assert(TM >= 1 && TN >= 1 && (BM + BN) % (kRowsPerLoad * NW) == 0 && BM % 8 == 0,
+                "tile shape");
   __shared__ Stage<BM, BN> ring[S];
 
-  const int bid = blockIdx.x;
+  // Workgroup b runs on XCD b % 8; XCD x takes the x-th contiguous run of
+  // tiles (ordered by group, then output columns, then rows), so each XCD's
+  // L2 holds the x rows of one or two groups instead of all of them.
+  const int bid = int(blockIdx.x % kXcds) * args.xcd_span + int(blockIdx.x / kXcds);
   int g = 0;
   while (g + 1 < args.ngroups && bid >= args.tile_end[g]) ++g;
   if (bid >= args.tile_end[g]) return;
@@ -124,17 +133,21 @@ __global__ __launch_bounds__(kProjThreads) void proj_kernel(const ProjArgs args)
   const int n0 = tn * BN;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % GM, wn = wave / GM;
   const int li = lane & 15, lg = lane >> 4;
+  // LDS destinations are wave-uniform: computed in scalar registers.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t ring_base = lds_addr(&ring[0].c[0]) + 1024u * wave_s;
+  constexpr uint32_t kStageBytes = sizeof(Stage<BM, BN>);
 
-  // Load i of this wave fills stage rows 8 j .. 8 j + 7, j = 4 i + wave; lane
+  // Load i of this wave fills stage rows 8 j .. 8 j + 7, j = NW i + wave; lane
   // l writes slot 8 row + q (row = 8 j + l / 8, q = l % 8), which holds
   // logical chunk q ^ (row & 7) of that row.
   const uint16_t* src[L];
   int chunk_k[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) {
-    const int row = kRowsPerLoad * (4 * i + wave) + (lane >> 3);
+    const int row = kRowsPerLoad * (NW * i + wave) + (lane >> 3);
     const int c = (lane & 7) ^ (row & 7);
     chunk_k[i] = 8 * c;
     if (row < BM) {
@@ -145,17 +158,21 @@ __global__ __launch_bounds__(kProjThreads) void proj_kernel(const ProjArgs args)
       src[i] = G.w + n * G.ldw + 8 * c;
     }
   }
-  // Issue stage kt's loads into `st`. Chunks past k (the 32-wide tail of the
-  // last stage) re-read a valid chunk; the tail stage never multiplies them.
+  // Issue stage kt's loads into ring slot `slot`. In the 32-wide tail stage
+  // (k % 64 == 32) chunks past k re-read a valid chunk; nothing multiplies
+  // them.
   const int nk = (K + 63) / 64;
-  auto issue = [&](int kt, Stage<BM, BN>& st) {
+  auto issue = [&](int kt, int slot) {
     const int k0 = kt * 64;
-    const bool tail = k0 + 64 > K;
+    const uint32_t base = ring_base + kStageBytes * slot;
+    if (k0 + 64 <= K) {
 #pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int off = (tail && k0 + chunk_k[i] >= K) ? K - 8 - chunk_k[i] : k0;
-      load_lds16(src[i] + off,
-                 __builtin_amdgcn_readfirstlane(lds_addr(&st.c[64 * (4 * i + wave)])));
+      for (int i = 0; i < L; ++i) load_lds16(src[i] + k0, base + 1024u * NW * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        load_lds16(src[i] + (k0 + chunk_k[i] >= K ? K - 8 - chunk_k[i] : k0),
+                   base + 1024u * NW * i);
     }
   };
 
@@ -165,33 +182,78 @@ __global__ __launch_bounds__(kProjThreads) void proj_kernel(const ProjArgs args)
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Stage<BM, BN>& st, int steps) {
-    for (int s = 0; s < steps; ++s) {
-      uint4 af[TM], bf[TN];
+  // A stage: all fragment reads first, then its MFMAs with the next stage's
+  // loads (when kIssue) spread between them, so the matrix core works while
+  // a load waits for the load pipe. Inline-assembly loads are scheduling
+  // boundaries, which keeps that placement.
+  auto stage = [&](int kt, auto steps_c, auto issue_c) {
+    constexpr int kSteps = decltype(steps_c)::value;
+    constexpr bool kIssue = decltype(issue_c)::value;
+    constexpr int kMfma = kSteps * TM * TN;
+    const Stage<BM, BN>& st = ring[kt % S];
+    uint4 af[kSteps][TM], bf[kSteps][TN];
 #pragma unroll
-      for (int a = 0; a < TM; ++a) af[a] = st.c[swz(wm * WM + a * 16 + li, 4 * s + lg)];
+    for (int s = 0; s < kSteps; ++s) {
 #pragma unroll
-      for (int b = 0; b < TN; ++b) bf[b] = st.c[swz(BM + wn * WN + b * 16 + li, 4 * s + lg)];
+      for (int a = 0; a < TM; ++a) af[s][a] = st.c[swz(wm * WM + a * 16 + li, 4 * s + lg)];
+#pragma unroll
+      for (int b = 0; b < TN; ++b) bf[s][b] = st.c[swz(BM + wn * WN + b * 16 + li, 4 * s + lg)];
+    }
+    const int k1 = (kt + S - 1) * 64;
+    const uint32_t base = ring_base + kStageBytes * ((kt + S - 1) % S);
+    int issued = 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = mma(af[a], bf[b], acc[a][b]);
+        for (int b = 0; b < TN; ++b) {
+          acc[a][b] = mma(af[s][a], bf[s][b], acc[a][b]);
+          if constexpr (kIssue) {
+            // load i goes after MFMA number ((i + 1) * kMfma) / (L + 1)
+            const int m = (s * TM + a) * TN + b + 1;
+#pragma unroll
+            for (int i = 0; i < L; ++i)
+              if (m == ((i + 1) * kMfma) / (L + 1) && issued == i) {
+                load_lds16(src[i] + k1, base + 1024u * NW * i);
+                ++issued;
+              }
+          }
+        }
+    if constexpr (kIssue) {
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        if (issued == i) {
+          load_lds16(src[i] + k1, base + 1024u * NW * i);
+          ++issued;
+        }
     }
   };
 
   // Stages 0 .. S-2 in flight before the loop. In iteration kt the wave waits
-  // until only the loads of stages kt+1 .. min(kt+S-2, nk-1) are pending, one
-  // barrier publishes stage kt to every wave and retires slot (kt-1) % S,
-  // whose reads all finished before it; that slot then receives stage
-  // kt + S - 1.
+  // until only the loads of stages kt+1 .. min(kt+S-2, nk-1) are pending and
+  // its LDS reads are done; one barrier publishes stage kt to every wave and
+  // retires slot (kt-1) % S, which receives stage kt + S - 1 while stage kt
+  // is multiplied. Only the last stage can be a 32-wide tail, and nothing is
+  // issued after it.
   static_assert(S >= 2 && S <= 8, "wait ladder covers rings of 2..8 stages");
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)
-    if (p < nk) issue(p, ring[p]);
+    if (p < nk) issue(p, p);
   for (int kt = 0; kt < nk; ++kt) {
     wait_pending<L, S - 2>(min(S - 2, nk - 1 - kt));
-    compute(ring[kt % S], min(2, (K - kt * 64) / 32));
-    if (kt + S - 1 < nk) issue(kt + S - 1, ring[(kt + S - 1) % S]);
+    if (kt + S - 1 < nk) {
+      if (kt + S - 1 == nk - 1 && (K & 63)) {
+        issue(kt + S - 1, (kt + S - 1) % S);  // the tail stage's clamped loads
+        stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
+      } else {
+        stage(kt, std::integral_constant<int, 2>{}, std::true_type{});
+      }
+    } else if (kt * 64 + 64 <= K) {
+      stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
+    } else {
+      stage(kt, std::integral_constant<int, 1>{}, std::false_type{});
+    }
   }
 
   const int act = G.act;
@@ -215,8 +277,9 @@ struct TileShape {
   int bm, bn;
 };
 
-// Tile shapes, largest first (fewest re-reads of x and w).
-constexpr TileShape kShapes[] = {{128, 64}, {64, 64}, {64, 32}};
+// Tile shapes, largest first (fewest re-reads of x and w); measured on the
+// MI355X inside HIP graphs.
+constexpr TileShape kShapes[] = {{64, 64}, {64, 32}, {32, 32}};
 
 int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) {
   int64_t tiles = 0;
@@ -225,7 +288,7 @@ int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) 
   return tiles;
 }
 
-template <int BM, int BN, int S>
+template <int BM, int BN, int S, int GM = 2, int GN = 2>
 int launch(int64_t m, const wkv7_proj_group* gs, int ng, hipStream_t s) {
   ProjArgs args{};
   args.m = m;
@@ -239,7 +302,8 @@ int launch(int64_t m, const wkv7_proj_group* gs, int ng, hipStream_t s) {
     args.tile_end[i] = int32_t(end);
   }
   args.tiles_m = int32_t(tiles_m);
-  proj_kernel<BM, BN, S><<<unsigned(end), kProjThreads, 0, s>>>(args);
+  args.xcd_span = int32_t((end + kXcds - 1) / kXcds);
+  proj_kernel<BM, BN, S, GM, GN><<<unsigned(args.xcd_span) * kXcds, 64 * GM * GN, 0, s>>>(args);
   return launch_status();
 }
 
@@ -268,22 +332,19 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return launch_status();
-  // The largest tile that still gives most compute units a workgroup; with
-  // short k (LoRA up-projections: a few stages per workgroup) aim for two
-  // workgroups per unit.
-  int kmax = 0;
-  for (int i = 0; i < ngroups; ++i) kmax = max(kmax, groups[i].k);
-  const int64_t target = kmax <= 256 ? 2 * int64_t(cus) : int64_t(cus) * 4 / 5;
+  // 64 x 64 tiles (8 waves) when they give every compute unit about two
+  // workgroups (one waits at its stage barrier while the other computes),
+  // else 64 x 32 tiles when they cover most units, else 32 x 32 tiles with
+  // a deeper ring.
   int pick = 2;
-  for (int i = 0; i < 3; ++i)
-    if (count_tiles(m, groups, ngroups, kShapes[i]) >= target) {
-      pick = i;
-      break;
-    }
+  if (count_tiles(m, groups, ngroups, kShapes[0]) * 2 >= int64_t(cus) * 3)
+    pick = 0;
+  else if (count_tiles(m, groups, ngroups, kShapes[1]) * 5 >= int64_t(cus) * 4)
+    pick = 1;
   hipStream_t s = as_stream(stream);
   switch (pick) {
-    case 0: return launch<128, 64, 4>(m, groups, ngroups, s);
-    case 1: return launch<64, 64, 4>(m, groups, ngroups, s);
-    default: return launch<64, 32, 4>(m, groups, ngroups, s);
+    case 0: return launch<64, 64, 4, 2, 4>(m, groups, ngroups, s);
+    case 1: return launch<64, 32, 4, 2, 2>(m, groups, ngroups, s);
+    default: return launch<32, 32, 8, 2, 2>(m, groups, ngroups, s);
   }
 }
