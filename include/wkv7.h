@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 6
+#define WKV7_ABI_VERSION 7
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -338,6 +338,37 @@ int wkv7_time_mix_output(int64_t total_tokens, int32_t H, const void *y, int32_t
                          const uint16_t *r, const uint16_t *k, const uint16_t *v,
                          const uint16_t *g, const uint16_t *r_k, const uint16_t *ln_w,
                          const uint16_t *ln_b, float eps, uint16_t *out, void *stream);
+
+/*
+ * The RWKV-7 time-mix decode of one token per slot, fused: for each batch
+ * row and head,
+ *     wkv7_time_mix_inputs -> wkv7_decode_slots (bf16 y) -> wkv7_time_mix_output
+ * in one workgroup, with the same arithmetic and the same bf16 roundings in
+ * the same order (the results are bit-identical to those three calls), but
+ * without the intermediate w, k, v, a, b and y rows in memory and with one
+ * launch instead of three.
+ *
+ * Replaces, for decode steps, the element-wise part of fla's RWKV7Attention
+ * around the wkv call together with the call itself (external; reached
+ * through the model forward, wkvm/runner/runner.py:80-88,
+ * wkvm/models/rwkv7.py:108-113).
+ *
+ *   wkv_layer, num_rows, H, slot_ids, row_order, B, scale: as wkv7_decode_slots
+ *   r, k, v, w_lora, a_lora, g        [B, H*64] bf16 projection / LoRA outputs
+ *   v_lora, v_first                   [B, H*64] bf16, both NULL for the first layer
+ *   k_k, k_a, r_k, ln_w, ln_b         [H*64] bf16 parameters; eps as wkv7_time_mix_output
+ *   out                               [B, H*64] bf16: the output projection's input
+ *   v_out                             [B, H*64] bf16 or NULL: the WKV op's v (the
+ *                                     first layer's is v_first for the others)
+ * Pointers must be 8-byte aligned (else WKV7_ERR_SHAPE).
+ */
+int wkv7_decode_block(float *wkv_layer, int64_t num_rows, int32_t H, const int32_t *slot_ids,
+                      const int32_t *row_order, int32_t B, const uint16_t *r, const uint16_t *k,
+                      const uint16_t *v, const uint16_t *w_lora, const uint16_t *a_lora,
+                      const uint16_t *v_lora, const uint16_t *v_first, const uint16_t *g,
+                      const uint16_t *k_k, const uint16_t *k_a, const uint16_t *r_k,
+                      const uint16_t *ln_w, const uint16_t *ln_b, float eps, float scale,
+                      uint16_t *out, uint16_t *v_out, void *stream);
 
 /*
  * Grouped projection GEMMs of the RWKV-7 time-mix block, for few rows (decode

@@ -324,3 +324,38 @@ def test_block_grouped_projections_match_vendor_path(dev, monkeypatch):
     rel = U.rel_l2(U.f64(outs[0]), U.f64(outs[1]))
     print(f"grouped vs vendor: state {err:.2e}, outputs rel-L2 {rel:.2e}")
     assert err <= 1e-2 and rel <= 1e-2
+
+
+@pytest.mark.parametrize("first_layer", [True, False])
+def test_decode_block_bit_identical_to_three_kernels(dev, first_layer):
+    """wkv7_decode_block equals time_mix_inputs -> wkv7_decode_slots (bf16 y)
+    -> time_mix_output bit for bit: output, v, and the state of every slot
+    (untouched slots included), with scattered slots in slot-sorted order."""
+    H, B, S = 8, 37, 60
+    D = H * 64
+    gen = torch.Generator(device=dev).manual_seed(120 + first_layer)
+
+    def bf(shape, std=1.0):
+        return (torch.randn(shape, generator=gen, device=dev) * std).to(torch.bfloat16)
+
+    r, k, v, wl, al, g = (bf((B, D)) for _ in range(6))
+    vl, vf = (None, None) if first_layer else (bf((B, D)), bf((B, D)))
+    k_k = (torch.rand(D, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+    k_a, ln_w = ((torch.rand(D, generator=gen, device=dev)).to(torch.bfloat16) for _ in range(2))
+    r_k, ln_b = bf(D, 0.1), bf(D, 0.05)
+    eps = 64e-5
+    pool = torch.randn((S + 1, H, 64, 64), generator=gen, device=dev) * 0.1
+    slots = (torch.randperm(S, generator=torch.Generator().manual_seed(7))[:B] + 1).tolist()
+    ids, order = ops.decode_plan(slots, S + 1, dev)
+    ref_pool = pool.clone()
+    w2, k2, v2, a2, b2 = ops.time_mix_inputs(H, k, v, wl, al, k_k, k_a, vl, vf)
+    vec = [t.view(B, H, 64) for t in (r, w2, k2, v2, a2, b2)]
+    y = ops.wkv7_decode_slots(ref_pool, ids, *vec, row_order=order)
+    ref = ops.time_mix_output(H, y, r, k2, v2, g, r_k, ln_w, ln_b, eps)
+    out, v_out = ops.wkv7_decode_block(pool, ids, H, r, k, v, wl, al, g, k_k, k_a, r_k, ln_w,
+                                       ln_b, eps, v_lora=vl, v_first=vf, row_order=order,
+                                       want_v=True)
+    torch.cuda.synchronize()
+    assert torch.equal(v_out, v2)
+    assert torch.equal(out, ref)
+    assert torch.equal(pool, ref_pool)

@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 6
+    assert lib.wkv7_abi_version() == 7
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():

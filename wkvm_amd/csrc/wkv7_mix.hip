@@ -17,20 +17,17 @@
 // (64 channels) is 16 lanes x 4 channels, so per-head sums are reductions
 // inside one 16-lane DPP row.
 #include "wkv7_common.h"
+#include "wkv7_timemix_head.h"
 
 namespace wkv7 {
 namespace {
 
 constexpr int kMixThreads = 256;
-constexpr float kLog2e = 1.4426950408889634f;
-// RWKV-7 log-decay scale: w = -exp(-0.5) * sigmoid(.) (decay in (0.545, 1))
-constexpr float kDecayScale = 0.6065306597126334f;
 
 struct Bf8 {
   uint32_t p[4];  // 8 bf16, element 2i in the low half of p[i]
 };
 
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ Bf8 ld8(const uint16_t* p) {
   const uint4 v = *reinterpret_cast<const uint4*>(p);
   return Bf8{{v.x, v.y, v.z, v.w}};
@@ -96,41 +93,6 @@ __global__ __launch_bounds__(kMixThreads) void token_shift_mix_kernel(
   }
 }
 
-// Four bf16 of a 16-lane head slice (8-byte loads).
-struct Bf4 {
-  uint32_t p[2];
-};
-__device__ __forceinline__ Bf4 ld4(const uint16_t* p) {
-  const uint2 v = *reinterpret_cast<const uint2*>(p);
-  return Bf4{{v.x, v.y}};
-}
-// Rows streamed once by time_mix_inputs / time_mix_output are read and written
-// with non-temporal hints (9-10 % faster than plain accesses; the token shift's
-// outputs are not: non-temporal stores made it 7 % slower).
-__device__ __forceinline__ Bf4 ld4_nt(const uint16_t* p) {
-  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
-  return Bf4{{v.x, v.y}};
-}
-__device__ __forceinline__ void st4(uint16_t* p, float a, float b, float c, float d) {
-  __builtin_nontemporal_store(u32x2_t{pack_bf16(a, b), pack_bf16(c, d)}, reinterpret_cast<u32x2_t*>(p));
-}
-__device__ __forceinline__ float el(const Bf4& v, int e) {
-  return (e & 1) ? bf16_hi(v.p[e >> 1]) : bf16_lo(v.p[e >> 1]);
-}
-
-// Sum over the 16 lanes of a DPP row (butterfly: every lane gets the total).
-__device__ __forceinline__ float row_sum16(float x) {
-  x += __shfl_xor(x, 1, 16);
-  x += __shfl_xor(x, 2, 16);
-  x += __shfl_xor(x, 4, 16);
-  x += __shfl_xor(x, 8, 16);
-  return x;
-}
-
-__device__ __forceinline__ float sigmoidf(float x) {
-  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
-}
-
 struct MixIn {
   const uint16_t *k, *v, *w_lora, *a_lora, *v_lora, *v_first, *k_k, *k_a;
 };
@@ -147,34 +109,29 @@ __global__ __launch_bounds__(kMixThreads) void time_mix_inputs_kernel(int64_t un
   const int64_t h = unit % H;
   const int64_t o = unit * kHead + 4 * sub;  // element offset: token row, head, channels
   const int pc = int(h * kHead + 4 * sub);   // parameter offset (channel within D)
-  const Bf4 k = ld4_nt(in.k + o), v = ld4_nt(in.v + o), wl = ld4_nt(in.w_lora + o),
-            al = ld4_nt(in.a_lora + o);
-  const Bf4 kk_s = ld4(in.k_k + pc), ka = ld4(in.k_a + pc);
-  float kk[4], a[4], ssq = 0.f;
+  const Bf4 kb = ld4_nt(in.k + o), vb = ld4_nt(in.v + o), wlb = ld4_nt(in.w_lora + o),
+            alb = ld4_nt(in.a_lora + o);
+  const Bf4 kksb = ld4(in.k_k + pc), kab = ld4(in.k_a + pc);
+  float k[4], v[4], wl[4], al[4], kks[4], ka[4], vl[4] = {}, vf[4] = {};
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    kk[e] = el(k, e) * el(kk_s, e);
-    ssq = fmaf(kk[e], kk[e], ssq);
-    a[e] = sigmoidf(el(al, e));
-  }
-  ssq = row_sum16(ssq);
-  // x / max(||x||, 1e-12), the F.normalize convention
-  const float inv = 1.f / fmaxf(sqrtf(ssq), 1e-12f);
-  float wv[4], kv[4], vv[4], av[4], bv[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float n = kk[e] * inv;
-    wv[e] = -kDecayScale * sigmoidf(el(wl, e));
-    kv[e] = el(k, e) * fmaf(a[e] - 1.f, el(ka, e), 1.f);
-    av[e] = -n;
-    bv[e] = n * a[e];
-    vv[e] = el(v, e);
+    k[e] = el(kb, e);
+    v[e] = el(vb, e);
+    wl[e] = el(wlb, e);
+    al[e] = el(alb, e);
+    kks[e] = el(kksb, e);
+    ka[e] = el(kab, e);
   }
   if (in.v_lora) {  // uniform: lerp(v, v_first, sigmoid(v_lora)) for layers > 0
-    const Bf4 vl = ld4_nt(in.v_lora + o), vf = ld4_nt(in.v_first + o);
+    const Bf4 vlb = ld4_nt(in.v_lora + o), vfb = ld4_nt(in.v_first + o);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) vv[e] = fmaf(el(vf, e) - vv[e], sigmoidf(el(vl, e)), vv[e]);
+    for (int e = 0; e < 4; ++e) {
+      vl[e] = el(vlb, e);
+      vf[e] = el(vfb, e);
+    }
   }
+  float wv[4], kv[4], vv[4], av[4], bv[4];
+  head_inputs(k, v, wl, al, kks, ka, in.v_lora != nullptr, vl, vf, wv, kv, vv, av, bv);
   st4(out.w + o, wv[0], wv[1], wv[2], wv[3]);
   st4(out.k + o, kv[0], kv[1], kv[2], kv[3]);
   st4(out.v + o, vv[0], vv[1], vv[2], vv[3]);
@@ -206,27 +163,21 @@ __global__ __launch_bounds__(kMixThreads) void time_mix_output_kernel(int64_t un
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = el(yv, e);
   }
-  const Bf4 r = ld4_nt(in.r + o), k = ld4_nt(in.k + o), v = ld4_nt(in.v + o), g = ld4_nt(in.g + o);
-  const Bf4 rk = ld4(in.r_k + pc), lw = ld4(in.ln_w + pc), lb = ld4(in.ln_b + pc);
-  float sum = 0.f, bonus = 0.f;
+  const Bf4 rb = ld4_nt(in.r + o), kb = ld4_nt(in.k + o), vb = ld4_nt(in.v + o),
+            gb = ld4_nt(in.g + o);
+  const Bf4 rkb = ld4(in.r_k + pc), lwb = ld4(in.ln_w + pc), lbb = ld4(in.ln_b + pc);
+  float r[4], k[4], v[4], g[4], rk[4], lw[4], lb[4], ov[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    sum += y[e];
-    bonus = fmaf(el(r, e) * el(k, e), el(rk, e), bonus);
+    r[e] = el(rb, e);
+    k[e] = el(kb, e);
+    v[e] = el(vb, e);
+    g[e] = el(gb, e);
+    rk[e] = el(rkb, e);
+    lw[e] = el(lwb, e);
+    lb[e] = el(lbb, e);
   }
-  const float mean = row_sum16(sum) * (1.f / kHead);
-  bonus = row_sum16(bonus);
-  float sq = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    y[e] -= mean;
-    sq = fmaf(y[e], y[e], sq);
-  }
-  const float rstd = 1.f / sqrtf(row_sum16(sq) * (1.f / kHead) + eps);  // biased variance
-  float ov[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    ov[e] = (fmaf(y[e] * rstd, el(lw, e), el(lb, e)) + bonus * el(v, e)) * el(g, e);
+  head_output(y, r, k, v, g, rk, lw, lb, eps, ov);
   st4(out + o, ov[0], ov[1], ov[2], ov[3]);
 }
 

@@ -703,6 +703,49 @@ def time_mix_output(H: int, y, r, k, v, g, r_k, ln_w, ln_b, eps: float,
     return o
 
 
+def wkv7_decode_block(wkv_layer: torch.Tensor, slot_ids, H: int, r, k, v, w_lora, a_lora, g,
+                      k_k, k_a, r_k, ln_w, ln_b, eps: float, *, v_lora=None, v_first=None,
+                      row_order=None, scale: float = 1.0, want_v: bool = False,
+                      out: torch.Tensor | None = None):
+    """The time-mix decode of one token per slot in one launch
+    (``wkv7_decode_block``): ``time_mix_inputs`` -> in-place WKV decode of
+    ``wkv_layer`` (bf16 y) -> ``time_mix_output``, bit-identical to those three
+    calls. Row vectors ``[B, H*64]`` bf16, parameters ``[H*64]``. Returns
+    ``out [B, H*64]`` (the output projection's input), and with ``want_v``
+    also the WKV op's v (the first layer's is v_first for the others)."""
+    rows, pool_heads = _check_pool(wkv_layer)
+    if pool_heads != int(H):
+        raise ValueError(f"pool has {pool_heads} heads, H = {H}")
+    dev = wkv_layer.device
+    ids = device_ids(slot_ids, rows, dev, "slot_ids")
+    B, D = int(ids.shape[0]), int(H) * HEAD_SIZE
+    if (v_lora is None) != (v_first is None):
+        raise ValueError("v_lora and v_first go together (both None for the first layer)")
+    vecs = [_bf16_2d(t, n, (B, D)) for t, n in ((r, "r"), (k, "k"), (v, "v"), (w_lora, "w_lora"),
+                                                 (a_lora, "a_lora"), (g, "g"))]
+    lora = [None, None] if v_lora is None else [_bf16_2d(v_lora, "v_lora", (B, D)),
+                                                 _bf16_2d(v_first, "v_first", (B, D))]
+    params = [_bf16_2d(t.reshape(-1), n, (D,)) for t, n in ((k_k, "k_k"), (k_a, "k_a"),
+                                                            (r_k, "r_k"), (ln_w, "ln_w"),
+                                                            (ln_b, "ln_b"))]
+    for t in vecs + params + [x for x in lora if x is not None]:
+        if t.device != dev:
+            raise ValueError("decode block tensors must share the pool's device")
+    o = _out(out, (B, D), torch.bfloat16, dev, "out")
+    v_out = torch.empty((B, D), dtype=torch.bfloat16, device=dev) if want_v else None
+    order = None
+    if row_order is not None:
+        order = device_ids(row_order, B, dev, "row_order")
+    if B:
+        rc = _lib.load().wkv7_decode_block(
+            wkv_layer.data_ptr(), rows, int(H), ids.data_ptr(), _ptr(order), B,
+            *(t.data_ptr() for t in vecs[:5]), _ptr(lora[0]), _ptr(lora[1]), vecs[5].data_ptr(),
+            *(t.data_ptr() for t in params), float(eps), float(scale), o.data_ptr(),
+            _ptr(v_out), _stream_ptr(dev))
+        _lib.check(rc, "wkv7_decode_block")
+    return (o, v_out) if want_v else o
+
+
 ACTIVATIONS = {None: _lib.WKV7_ACT_NONE, "tanh": _lib.WKV7_ACT_TANH,
                "sigmoid": _lib.WKV7_ACT_SIGMOID}
 

@@ -16,8 +16,10 @@ place, and every element-wise stage is one of this library's kernels:
                             second stages with their biases) and one for o;
                             above that the vendor BLAS through torch's linear
     -> time_mix_inputs      log-decay w, k, v (v_first lerp), a = -kk, b = kk*a
-    -> WKV7                 wkv7_decode_slots (one token per slot) or
-                            wkv7_prefill_varlen (ragged), bank.wkv[l] in place
+    -> WKV7                 wkv7_prefill_varlen (ragged), bank.wkv[l] in place;
+                            for one token per slot, wkv7_decode_block runs
+                            time_mix_inputs, the in-place decode and
+                            time_mix_output as one launch
     -> time_mix_output      per-head GroupNorm, bonus, gate
     -> o_proj
 
@@ -216,9 +218,16 @@ class RWKV7TimeMix:
         return ops.proj_grouped([(o_in, W["o"])])[0], v_first
 
     def _wkv_stage(self, bank, batch, v_first, zero_init, r, k, v, w_l, a_l, v_l, g):
-        """time_mix_inputs -> in-place WKV7 -> time_mix_output; returns the
-        output projection's input and v_first."""
+        """time_mix_inputs -> in-place WKV7 -> time_mix_output (one fused
+        launch for decode batches); returns the output projection's input and
+        v_first."""
         W, l, H = self.w, self.layer_idx, self.layout.num_heads
+        if batch.decode:
+            res = ops.wkv7_decode_block(
+                bank.wkv[l], batch.slot_ids, H, r, k, v, w_l, a_l, g, W["k_k"], W["k_a"],
+                W["r_k"], W["ln_w"], W["ln_b"], self.eps, v_lora=v_l,
+                v_first=v_first if l > 0 else None, row_order=batch.order, want_v=(l == 0))
+            return res if l == 0 else (res, v_first)
         w, k2, v2, a, b = ops.time_mix_inputs(H, k, v, w_l, a_l, W["k_k"], W["k_a"], v_l,
                                               v_first if l > 0 else None)
         if l == 0:
