@@ -110,6 +110,51 @@ def test_abi_rejects_bad_arguments_before_any_launch():
         assert _lib.strerror(code)
 
 
+def test_abi_rejects_bad_projection_and_decode_block_arguments():
+    """wkv7_proj_grouped and wkv7_decode_block validate everything before any
+    device call (CPU-runnable), and zero rows is a successful no-op."""
+    lib = _lib.load()
+    G = _lib.ProjGroup
+
+    def groups(**kw):
+        base = dict(x=4096, w=8192, bias=None, y=12288, ldx=64, ldw=64, ldy=32, n=32, k=64,
+                    act=_lib.WKV7_ACT_NONE, reserved=0)
+        base.update(kw)
+        arr = (G * 1)()
+        arr[0] = G(**base)
+        return arr
+
+    ok = groups()
+    assert lib.wkv7_proj_grouped(0, ok, 1, None) == _lib.WKV7_OK
+    assert lib.wkv7_proj_grouped(-1, ok, 1, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, ok, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, ok, _lib.WKV7_PROJ_MAX_GROUPS + 1, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, None, 1, None) == _lib.WKV7_ERR_ARG
+    for bad in (dict(k=48), dict(k=0), dict(n=0), dict(act=3), dict(x=None), dict(w=None),
+                dict(y=None)):
+        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None) == _lib.WKV7_ERR_ARG, bad
+    for bad in (dict(ldx=32), dict(ldw=68), dict(ldy=16), dict(x=4100), dict(w=8200)):
+        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None) == _lib.WKV7_ERR_SHAPE, bad
+
+    d = ctypes.c_void_p(4096)
+
+    def block(B=1, H=2, eps=64e-5, r=d, v_lora=None, v_first=None, out=d, v_out=None):
+        return lib.wkv7_decode_block(d, 5, H, d, None, B, r, d, d, d, d, v_lora, v_first, d, d,
+                                     d, d, d, d, eps, 1.0, out, v_out, None)
+
+    assert block(B=0) == _lib.WKV7_OK
+    assert block(B=-1) == _lib.WKV7_ERR_ARG
+    assert block(H=0) == _lib.WKV7_ERR_ARG
+    assert block(eps=-1.0) == _lib.WKV7_ERR_ARG
+    assert block(eps=float("nan")) == _lib.WKV7_ERR_ARG
+    assert block(r=None) == _lib.WKV7_ERR_ARG
+    assert block(out=None) == _lib.WKV7_ERR_ARG
+    assert block(v_lora=d) == _lib.WKV7_ERR_ARG  # v_lora without v_first
+    assert block(r=ctypes.c_void_p(4100)) == _lib.WKV7_ERR_SHAPE
+    assert block(v_lora=d, v_first=ctypes.c_void_p(4098)) == _lib.WKV7_ERR_SHAPE
+    assert block(v_out=ctypes.c_void_p(4097)) == _lib.WKV7_ERR_SHAPE
+
+
 def test_check_maps_codes_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.WKV7_ERR_ARG, "x")
