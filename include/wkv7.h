@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 7
+#define WKV7_ABI_VERSION 8
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -411,7 +411,14 @@ typedef struct wkv7_proj_group {
 } wkv7_proj_group;
 
 int wkv7_proj_grouped(int64_t m, const wkv7_proj_group *groups, int32_t ngroups,
-                      void *stream);
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace wkv7_proj_grouped can use for these products on the current
+ * device (0: none). With at least this many bytes (16-byte aligned) it may
+ * split long k over several workgroups, whose fp32 partials a second kernel
+ * sums in a fixed order; with less it runs unsplit. Both give results within
+ * one bf16 ulp of the exact product; each is deterministic. */
+size_t wkv7_proj_workspace_bytes(int64_t m, const wkv7_proj_group *groups, int32_t ngroups);
 
 #ifdef __cplusplus
 }

@@ -127,3 +127,36 @@ def test_rejected_arguments(dev):
         ops.proj_grouped([(x, w, None, "relu")])
     with pytest.raises(ValueError, match="same row count"):
         ops.proj_grouped([(x, w), (x[:2], w)])
+
+
+def test_split_k_partials_and_unsplit_fallback(dev):
+    """A long-k product with few rows splits k over several workgroups when
+    given the workspace it asks for (the last part holding the 32-wide k
+    tail), and runs unsplit without one. Both are within one bf16 ulp of the
+    exact product and each repeats bit for bit."""
+    from wkvm_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(31)
+    M, K, N = 5, 1056, 2048
+    x = _rand((M, K), gen, dev)
+    w = _rand((N, K), gen, dev, 1 / math.sqrt(K))
+    b = _rand((N,), gen, dev)
+    exact = _exact(x, w, b, "tanh")
+    arr = (_lib.ProjGroup * 1)()
+    outs = []
+    for use_ws in (True, False, True):
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        arr[0] = _lib.ProjGroup(x.data_ptr(), w.data_ptr(), b.data_ptr(), y.data_ptr(), K, K, N,
+                                N, K, _lib.WKV7_ACT_TANH, 0)
+        ws_bytes = int(lib.wkv7_proj_workspace_bytes(M, arr, 1)) if use_ws else 0
+        if use_ws:
+            assert ws_bytes > 0, "few rows and long k should ask for a split-k workspace"
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        rc = lib.wkv7_proj_grouped(M, arr, 1, ws.data_ptr() if use_ws else None, ws_bytes,
+                                   torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        _assert_within_one_ulp(y, exact)
+        outs.append(y)
+    assert torch.equal(outs[0], outs[2])

@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 7
+    assert lib.wkv7_abi_version() == 8
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():
@@ -125,16 +125,18 @@ def test_abi_rejects_bad_projection_and_decode_block_arguments():
         return arr
 
     ok = groups()
-    assert lib.wkv7_proj_grouped(0, ok, 1, None) == _lib.WKV7_OK
-    assert lib.wkv7_proj_grouped(-1, ok, 1, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_proj_grouped(4, ok, 0, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_proj_grouped(4, ok, _lib.WKV7_PROJ_MAX_GROUPS + 1, None) == _lib.WKV7_ERR_ARG
-    assert lib.wkv7_proj_grouped(4, None, 1, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(0, ok, 1, None, 0, None) == _lib.WKV7_OK
+    assert lib.wkv7_proj_workspace_bytes(0, ok, 1) == 0  # no rows: nothing to split
+    assert lib.wkv7_proj_workspace_bytes(4, groups(k=48), 1) == 0  # rejected: no workspace
+    assert lib.wkv7_proj_grouped(-1, ok, 1, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, ok, 0, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, ok, _lib.WKV7_PROJ_MAX_GROUPS + 1, None, 0, None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_proj_grouped(4, None, 1, None, 0, None) == _lib.WKV7_ERR_ARG
     for bad in (dict(k=48), dict(k=0), dict(n=0), dict(act=3), dict(x=None), dict(w=None),
                 dict(y=None)):
-        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None) == _lib.WKV7_ERR_ARG, bad
+        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None, 0, None) == _lib.WKV7_ERR_ARG, bad
     for bad in (dict(ldx=32), dict(ldw=68), dict(ldy=16), dict(x=4100), dict(w=8200)):
-        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None) == _lib.WKV7_ERR_SHAPE, bad
+        assert lib.wkv7_proj_grouped(4, groups(**bad), 1, None, 0, None) == _lib.WKV7_ERR_SHAPE, bad
 
     d = ctypes.c_void_p(4096)
 

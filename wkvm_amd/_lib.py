@@ -77,7 +77,8 @@ SIGNATURES = {
         _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "wkv7_time_mix_output": (ctypes.c_int, [
         _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
-    "wkv7_proj_grouped": (ctypes.c_int, [_i64, ctypes.POINTER(ProjGroup), _i32, _vp]),
+    "wkv7_proj_grouped": (ctypes.c_int, [_i64, ctypes.POINTER(ProjGroup), _i32, _vp, _sz, _vp]),
+    "wkv7_proj_workspace_bytes": (_sz, [_i64, ctypes.POINTER(ProjGroup), _i32]),
     "wkv7_decode_block": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _i32] + [_vp] * 13 + [_f32, _f32, _vp, _vp, _vp]),
 }

@@ -22,6 +22,7 @@
 // stage. Rows past m and columns past n load a clamped (valid) row and are
 // not stored. Tiles are dealt to the XCDs in contiguous runs so that each
 // XCD's L2 keeps the x rows it re-reads.
+#include <algorithm>
 #include <type_traits>
 
 #include "wkv7_common.h"
@@ -38,11 +39,15 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt round-robin over 8 XCD
 
 struct ProjArgs {
   wkv7_proj_group g[WKV7_PROJ_MAX_GROUPS];
-  int32_t tile_end[WKV7_PROJ_MAX_GROUPS];  // exclusive prefix sums of tiles per group
+  int32_t tile_end[WKV7_PROJ_MAX_GROUPS];  // exclusive prefix sums of work items per group
+  int64_t ws_off[WKV7_PROJ_MAX_GROUPS];    // split k: group's partials, [parts][m][n] fp32
+  int64_t elem_end[WKV7_PROJ_MAX_GROUPS];  // split k: prefix sums of m * n
+  float* ws;
   int64_t m;
   int32_t tiles_m;
   int32_t ngroups;
-  int32_t xcd_span;  // tiles per XCD: ceil(tiles / kXcds)
+  int32_t xcd_span;  // work items per XCD: ceil(items / kXcds)
+  int32_t parts;     // k parts per output tile (1: the tile's workgroup covers all of k)
 };
 
 __device__ __forceinline__ f32x4 mma(const uint4& a, const uint4& b, f32x4 c) {
@@ -104,7 +109,7 @@ __device__ __forceinline__ void wait_pending(int pending) {
   }
 }
 
-template <int BM, int BN, int S, int GM, int GN>
+template <int BM, int BN, int S, int GM, int GN, bool kSplit>
 __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args) {
   constexpr int NW = GM * GN;                 // waves, a GM x GN grid
   constexpr int WM = BM / GM, WN = BN / GN;   // wave tile
@@ -125,7 +130,9 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
   while (g + 1 < args.ngroups && bid >= args.tile_end[g]) ++g;
   if (bid >= args.tile_end[g]) return;
   const wkv7_proj_group& G = args.g[g];
-  const int local = bid - (g ? args.tile_end[g - 1] : 0);
+  const int item = bid - (g ? args.tile_end[g - 1] : 0);
+  const int part = kSplit ? item % args.parts : 0;
+  const int local = kSplit ? item / args.parts : item;
   const int tm = local % args.tiles_m, tn = local / args.tiles_m;
   const int64_t M = args.m;
   const int N = G.n, K = G.k;
@@ -161,9 +168,15 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
   // Issue stage kt's loads into ring slot `slot`. In the 32-wide tail stage
   // (k % 64 == 32) chunks past k re-read a valid chunk; nothing multiplies
   // them.
-  const int nk = (K + 63) / 64;
+  // This workgroup's k stages: [kb, kb + nk) of the product's nk_all, all
+  // of them unless k is split over `parts` workgroups.
+  const int nk_all = (K + 63) / 64;
+  const int spp = kSplit ? (nk_all + args.parts - 1) / args.parts : nk_all;
+  const int kb = kSplit ? min(part * spp, nk_all) : 0;
+  const int nk = kSplit ? min(nk_all, kb + spp) - kb : nk_all;
+  const bool has_tail = (K & 63) && kb + nk == nk_all;  // the 32-wide tail stage is ours
   auto issue = [&](int kt, int slot) {
-    const int k0 = kt * 64;
+    const int k0 = (kb + kt) * 64;
     const uint32_t base = ring_base + kStageBytes * slot;
     if (k0 + 64 <= K) {
 #pragma unroll
@@ -191,6 +204,7 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
     constexpr bool kIssue = decltype(issue_c)::value;
     constexpr int kMfma = kSteps * TM * TN;
     const Stage<BM, BN>& st = ring[kt % S];
+    // (kt counts this workgroup's stages; k offsets add kb)
     uint4 af[kSteps][TM], bf[kSteps][TN];
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
@@ -199,7 +213,7 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
 #pragma unroll
       for (int b = 0; b < TN; ++b) bf[s][b] = st.c[swz(BM + wn * WN + b * 16 + li, 4 * s + lg)];
     }
-    const int k1 = (kt + S - 1) * 64;
+    const int k1 = (kb + kt + S - 1) * 64;
     const uint32_t base = ring_base + kStageBytes * ((kt + S - 1) % S);
     int issued = 0;
 #pragma unroll
@@ -243,19 +257,35 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
   for (int kt = 0; kt < nk; ++kt) {
     wait_pending<L, S - 2>(min(S - 2, nk - 1 - kt));
     if (kt + S - 1 < nk) {
-      if (kt + S - 1 == nk - 1 && (K & 63)) {
+      if (kt + S - 1 == nk - 1 && has_tail) {
         issue(kt + S - 1, (kt + S - 1) % S);  // the tail stage's clamped loads
         stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
       } else {
         stage(kt, std::integral_constant<int, 2>{}, std::true_type{});
       }
-    } else if (kt * 64 + 64 <= K) {
+    } else if ((kb + kt) * 64 + 64 <= K) {
       stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
     } else {
       stage(kt, std::integral_constant<int, 1>{}, std::false_type{});
     }
   }
 
+  if constexpr (kSplit) {  // fp32 partial tile; proj_reduce_kernel finishes the sum
+    float* wsp = args.ws + args.ws_off[g] + int64_t(part) * M * N;
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int col = n0 + wn * WN + b * 16 + li;
+      if (col >= N) continue;
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t row = m0 + wm * WM + a * 16 + 4 * lg + e;
+          if (row < M) wsp[row * N + col] = acc[a][b][e];
+        }
+    }
+    return;
+  }
   const int act = G.act;
 #pragma unroll
   for (int b = 0; b < TN; ++b) {
@@ -271,6 +301,25 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
       }
     }
   }
+}
+
+// Split k: y = act(sum of the k parts' partials, in part order, + bias), one
+// thread per output element.
+__global__ __launch_bounds__(256) void proj_reduce_kernel(const ProjArgs args) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  int g = 0;
+  while (g + 1 < args.ngroups && e >= args.elem_end[g]) ++g;
+  if (e >= args.elem_end[g]) return;
+  const wkv7_proj_group& G = args.g[g];
+  const int64_t local = e - (g ? args.elem_end[g - 1] : 0);
+  const int64_t row = local / G.n;
+  const int col = int(local - row * G.n);
+  const int64_t plane = args.m * G.n;
+  const float* src = args.ws + args.ws_off[g] + local;
+  float sum = 0.f;
+  for (int p = 0; p < args.parts; ++p) sum += src[p * plane];
+  const float bias = G.bias ? bf16_to_f32(G.bias[col]) : 0.f;
+  G.y[row * G.ldy + col] = f32_to_bf16(activate(sum + bias, G.act));
 }
 
 struct TileShape {
@@ -289,23 +338,84 @@ int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) 
 }
 
 template <int BM, int BN, int S, int GM = 2, int GN = 2>
-int launch(int64_t m, const wkv7_proj_group* gs, int ng, hipStream_t s) {
+int launch(int64_t m, const wkv7_proj_group* gs, int ng, int parts, float* ws, hipStream_t s) {
   ProjArgs args{};
   args.m = m;
   args.ngroups = ng;
+  args.parts = parts;
+  args.ws = ws;
   const int64_t tiles_m = (m + BM - 1) / BM;
-  int64_t end = 0;
+  int64_t end = 0, elems = 0;
   for (int i = 0; i < ng; ++i) {
     args.g[i] = gs[i];
-    end += tiles_m * ((gs[i].n + BN - 1) / BN);
+    end += tiles_m * ((gs[i].n + BN - 1) / BN) * parts;
     if (end > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
     args.tile_end[i] = int32_t(end);
+    args.ws_off[i] = elems * parts;
+    elems += m * gs[i].n;
+    args.elem_end[i] = elems;
   }
   args.tiles_m = int32_t(tiles_m);
   args.xcd_span = int32_t((end + kXcds - 1) / kXcds);
-  proj_kernel<BM, BN, S, GM, GN><<<unsigned(args.xcd_span) * kXcds, 64 * GM * GN, 0, s>>>(args);
+  const unsigned grid = unsigned(args.xcd_span) * kXcds;
+  if (parts == 1) {
+    proj_kernel<BM, BN, S, GM, GN, false><<<grid, 64 * GM * GN, 0, s>>>(args);
+  } else {
+    proj_kernel<BM, BN, S, GM, GN, true><<<grid, 64 * GM * GN, 0, s>>>(args);
+    const int rc = launch_status();
+    if (rc != WKV7_OK) return rc;
+    const int64_t blocks = (elems + 255) / 256;
+    if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
+    proj_reduce_kernel<<<unsigned(blocks), 256, 0, s>>>(args);
+  }
   return launch_status();
 }
+
+// Tile shape and k split for a launch (the same decision for the workspace
+// query and the launch).
+struct Plan {
+  int shape;  // index into kShapes
+  int parts;  // k parts per tile
+  size_t ws_bytes;
+};
+
+Plan make_plan(int64_t m, const wkv7_proj_group* gs, int ng, int cus) {
+  // 64 x 64 tiles (8 waves) when they give every compute unit about two
+  // workgroups (one waits at its stage barrier while the other computes),
+  // else 64 x 32 tiles when they cover most units, else 32 x 32 tiles with
+  // a deeper ring.
+  Plan p{2, 1, 0};
+  int64_t tiles = count_tiles(m, gs, ng, kShapes[2]);
+  if (count_tiles(m, gs, ng, kShapes[0]) * 2 >= int64_t(cus) * 3) {
+    p.shape = 0;
+    tiles = count_tiles(m, gs, ng, kShapes[0]);
+  } else if (count_tiles(m, gs, ng, kShapes[1]) * 5 >= int64_t(cus) * 4) {
+    p.shape = 1;
+    tiles = count_tiles(m, gs, ng, kShapes[1]);
+  }
+  // At most one workgroup per two units and long k: split k so that about two
+  // workgroups per unit each walk at least 8 stages. (With more tiles the
+  // partials' extra traffic and second launch cost more than they save.)
+  int kmin = gs[0].k;
+  int64_t cols = 0;
+  for (int i = 0; i < ng; ++i) {
+    kmin = std::min(kmin, gs[i].k);
+    cols += gs[i].n;
+  }
+  const int nk = (kmin + 63) / 64;
+  if (tiles * 2 <= int64_t(cus) && nk >= 16) {
+    int64_t parts = (2 * int64_t(cus) + tiles / 2) / tiles;
+    parts = std::min<int64_t>(parts, std::min(8, nk / 8));
+    if (parts >= 2) {
+      p.parts = int(parts);
+      p.ws_bytes = size_t(parts) * size_t(m) * size_t(cols) * sizeof(float);
+    }
+  }
+  return p;
+}
+
+int validate(int64_t m, const wkv7_proj_group* groups, int32_t ngroups);
+int device_cus(int* cus);
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -314,8 +424,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace wkv7;
 
-extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32_t ngroups,
-                                 void* stream) {
+namespace wkv7 {
+namespace {
+
+int validate(int64_t m, const wkv7_proj_group* groups, int32_t ngroups) {
   if (m < 0 || !groups || ngroups < 1 || ngroups > WKV7_PROJ_MAX_GROUPS) return WKV7_ERR_ARG;
   if (m > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
   for (int i = 0; i < ngroups; ++i) {
@@ -326,25 +438,45 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
     if (g.ldx < g.k || g.ldw < g.k || g.ldy < g.n) return WKV7_ERR_SHAPE;
     if (g.ldx % 8 || g.ldw % 8 || !aligned16(g.x) || !aligned16(g.w)) return WKV7_ERR_SHAPE;
   }
-  if (m == 0) return WKV7_OK;
-  int cus = 0;
+  return WKV7_OK;
+}
+
+int device_cus(int* cus) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return launch_status();
-  // 64 x 64 tiles (8 waves) when they give every compute unit about two
-  // workgroups (one waits at its stage barrier while the other computes),
-  // else 64 x 32 tiles when they cover most units, else 32 x 32 tiles with
-  // a deeper ring.
-  int pick = 2;
-  if (count_tiles(m, groups, ngroups, kShapes[0]) * 2 >= int64_t(cus) * 3)
-    pick = 0;
-  else if (count_tiles(m, groups, ngroups, kShapes[1]) * 5 >= int64_t(cus) * 4)
-    pick = 1;
+  return WKV7_OK;
+}
+
+}  // namespace
+}  // namespace wkv7
+
+extern "C" size_t wkv7_proj_workspace_bytes(int64_t m, const wkv7_proj_group* groups,
+                                            int32_t ngroups) {
+  if (validate(m, groups, ngroups) != WKV7_OK || m == 0) return 0;
+  int cus = 0;
+  if (device_cus(&cus) != WKV7_OK) return 0;
+  return make_plan(m, groups, ngroups, cus).ws_bytes;
+}
+
+extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32_t ngroups,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = validate(m, groups, ngroups);
+  if (rc != WKV7_OK) return rc;
+  if (m == 0) return WKV7_OK;
+  int cus = 0;
+  const int drc = device_cus(&cus);
+  if (drc != WKV7_OK) return drc;
+  Plan p = make_plan(m, groups, ngroups, cus);
+  // without (enough) workspace every tile's workgroup covers all of k
+  if (p.parts > 1 && (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)))
+    p.parts = 1;
+  float* ws = static_cast<float*>(workspace);
   hipStream_t s = as_stream(stream);
-  switch (pick) {
-    case 0: return launch<64, 64, 4, 2, 4>(m, groups, ngroups, s);
-    case 1: return launch<64, 32, 4, 2, 2>(m, groups, ngroups, s);
-    default: return launch<32, 32, 8, 2, 2>(m, groups, ngroups, s);
+  switch (p.shape) {
+    case 0: return launch<64, 64, 4, 2, 4>(m, groups, ngroups, p.parts, ws, s);
+    case 1: return launch<64, 32, 4, 2, 2>(m, groups, ngroups, p.parts, ws, s);
+    default: return launch<32, 32, 8, 2, 2>(m, groups, ngroups, p.parts, ws, s);
   }
 }

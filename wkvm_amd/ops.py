@@ -806,8 +806,13 @@ def proj_grouped(products: Sequence[tuple], outs: Sequence[torch.Tensor | None] 
         keep += [x, w, bias]
         ys.append(y)
     if M:
-        rc = _lib.load().wkv7_proj_grouped(M, groups, len(products),
-                                           _stream_ptr(ys[0].device))
+        lib = _lib.load()
+        n = len(products)
+        ws_bytes = int(lib.wkv7_proj_workspace_bytes(M, groups, n))
+        ws = (torch.empty(ws_bytes, dtype=torch.uint8, device=ys[0].device) if ws_bytes
+              else None)
+        rc = lib.wkv7_proj_grouped(M, groups, n, _ptr(ws), ws_bytes,
+                                   _stream_ptr(ys[0].device))
         _lib.check(rc, "wkv7_proj_grouped")
     return ys
 
