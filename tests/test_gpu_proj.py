@@ -160,3 +160,26 @@ def test_split_k_partials_and_unsplit_fallback(dev):
         _assert_within_one_ulp(y, exact)
         outs.append(y)
     assert torch.equal(outs[0], outs[2])
+
+
+def test_split_k_over_several_groups(dev):
+    """Several products with few rows split k together (different n, one
+    with bias and sigmoid); every output within one bf16 ulp."""
+    from wkvm_amd import _lib
+
+    gen = torch.Generator().manual_seed(41)
+    M, K = 3, 2048
+    x1, x2 = _rand((M, K), gen, dev), _rand((M, K), gen, dev)
+    w1 = _rand((2048, K), gen, dev, 1 / math.sqrt(K))
+    w2 = _rand((96, K), gen, dev, 1 / math.sqrt(K))
+    b2 = _rand((96,), gen, dev)
+    ys = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=dev) for w in (w1, w2)]
+    arr = (_lib.ProjGroup * 2)()
+    for i, (x, w, b, a) in enumerate(((x1, w1, None, None), (x2, w2, b2, "sigmoid"))):
+        arr[i] = _lib.ProjGroup(x.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(),
+                                ys[i].data_ptr(), K, K, w.shape[0], w.shape[0], K,
+                                ops.ACTIVATIONS[a], 0)
+    assert _lib.load().wkv7_proj_workspace_bytes(M, arr, 2) > 0, "expected a split-k plan"
+    y1, y2 = ops.proj_grouped([(x1, w1), (x2, w2, b2, "sigmoid")], outs=ys)
+    _assert_within_one_ulp(y1, _exact(x1, w1, None, None))
+    _assert_within_one_ulp(y2, _exact(x2, w2, b2, "sigmoid"))

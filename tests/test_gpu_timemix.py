@@ -326,11 +326,12 @@ def test_block_grouped_projections_match_vendor_path(dev, monkeypatch):
     assert err <= 1e-2 and rel <= 1e-2
 
 
-@pytest.mark.parametrize("first_layer", [True, False])
-def test_decode_block_bit_identical_to_three_kernels(dev, first_layer):
+@pytest.mark.parametrize("first_layer,scale", [(True, 1.0), (False, 1.0), (False, 0.5)])
+def test_decode_block_bit_identical_to_three_kernels(dev, first_layer, scale):
     """wkv7_decode_block equals time_mix_inputs -> wkv7_decode_slots (bf16 y)
     -> time_mix_output bit for bit: output, v, and the state of every slot
-    (untouched slots included), with scattered slots in slot-sorted order."""
+    (untouched slots included), with scattered slots in slot-sorted order.
+    scale multiplies r in the state readout only (the bonus uses raw r)."""
     H, B, S = 8, 37, 60
     D = H * 64
     gen = torch.Generator(device=dev).manual_seed(120 + first_layer)
@@ -350,11 +351,11 @@ def test_decode_block_bit_identical_to_three_kernels(dev, first_layer):
     ref_pool = pool.clone()
     w2, k2, v2, a2, b2 = ops.time_mix_inputs(H, k, v, wl, al, k_k, k_a, vl, vf)
     vec = [t.view(B, H, 64) for t in (r, w2, k2, v2, a2, b2)]
-    y = ops.wkv7_decode_slots(ref_pool, ids, *vec, row_order=order)
+    y = ops.wkv7_decode_slots(ref_pool, ids, *vec, row_order=order, scale=scale)
     ref = ops.time_mix_output(H, y, r, k2, v2, g, r_k, ln_w, ln_b, eps)
     out, v_out = ops.wkv7_decode_block(pool, ids, H, r, k, v, wl, al, g, k_k, k_a, r_k, ln_w,
                                        ln_b, eps, v_lora=vl, v_first=vf, row_order=order,
-                                       want_v=True)
+                                       scale=scale, want_v=True)
     torch.cuda.synchronize()
     assert torch.equal(v_out, v2)
     assert torch.equal(out, ref)
