@@ -33,7 +33,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kChunks = 8;  // 16-byte chunks per 64-wide k stage of a row
 
 constexpr int kXcds = 8;  // MI355X: workgroups are dealt round-robin over 8 XCDs
 
@@ -55,7 +54,10 @@ __device__ __forceinline__ f32x4 mma(const uint4& a, const uint4& b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ (row & 7)); }
+template <int KC>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return row * KC + (chunk ^ (row & (KC - 1)));
+}
 
 __device__ __forceinline__ float activate(float v, int act) {
   if (act == WKV7_ACT_TANH) return tanhf(v);
@@ -63,11 +65,11 @@ __device__ __forceinline__ float activate(float v, int act) {
   return v;
 }
 
-// One stage of the LDS ring: the A rows (x) then the B rows (w) of a 64-wide
-// k block, 8 swizzled 16-byte chunks per row.
-template <int BM, int BN>
+// One stage of the LDS ring: the A rows (x) then the B rows (w) of a
+// (8 KC)-wide k block, KC swizzled 16-byte chunks per row.
+template <int BM, int BN, int KC>
 struct Stage {
-  uint4 c[(BM + BN) * kChunks];
+  uint4 c[(BM + BN) * KC];
 };
 
 typedef __attribute__((address_space(3))) uint4 lds_uint4;
@@ -109,18 +111,21 @@ __device__ __forceinline__ void wait_pending(int pending) {
   }
 }
 
-template <int BM, int BN, int S, int GM, int GN, bool kSplit>
+template <int BM, int BN, int S, int GM, int GN, int BK, bool kSplit>
 __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args) {
   constexpr int NW = GM * GN;                 // waves, a GM x GN grid
   constexpr int WM = BM / GM, WN = BN / GN;   // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;   // accumulator tiles per wave
-  // Each wave-wide direct load fills 1 KiB of a stage = 8 rows; a thread
+  // k per stage BK = 64 or 128: KC chunks of 16 bytes per row. Each
+  // wave-wide direct load fills 1 KiB of a stage = 64 / KC rows; a thread
   // issues L of them per stage.
-  constexpr int kRowsPerLoad = 8;
+  constexpr int KC = BK / 8, kStepsFull = BK / 32;
+  static_assert(BK == 64 || BK == 128, "stage depth");
+  constexpr int kRowsPerLoad = 64 / KC;
   constexpr int L = (BM + BN) / (kRowsPerLoad * NW);
   static_assert(TM >= 1 && TN >= 1 && (BM + BN) % (kRowsPerLoad * NW) == 0 && BM % 8 == 0,
                 "tile shape");
-  __shared__ Stage<BM, BN> ring[S];
+  __shared__ Stage<BM, BN, KC> ring[S];
 
   // Workgroup b runs on XCD b % 8; XCD x takes the x-th contiguous run of
   // tiles (ordered by group, then output columns, then rows), so each XCD's
@@ -145,17 +150,17 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
   // LDS destinations are wave-uniform: computed in scalar registers.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ring_base = lds_addr(&ring[0].c[0]) + 1024u * wave_s;
-  constexpr uint32_t kStageBytes = sizeof(Stage<BM, BN>);
+  constexpr uint32_t kStageBytes = sizeof(Stage<BM, BN, KC>);
 
-  // Load i of this wave fills stage rows 8 j .. 8 j + 7, j = NW i + wave; lane
-  // l writes slot 8 row + q (row = 8 j + l / 8, q = l % 8), which holds
-  // logical chunk q ^ (row & 7) of that row.
+  // Load i of this wave fills stage rows R j .. R j + R - 1 (R = 64 / KC,
+  // j = NW i + wave); lane l writes slot KC row + q (row = R j + l / KC,
+  // q = l % KC), which holds logical chunk q ^ (row & (KC - 1)) of that row.
   const uint16_t* src[L];
   int chunk_k[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) {
-    const int row = kRowsPerLoad * (NW * i + wave) + (lane >> 3);
-    const int c = (lane & 7) ^ (row & 7);
+    const int row = kRowsPerLoad * (NW * i + wave) + lane / KC;
+    const int c = (lane % KC) ^ (row & (KC - 1));
     chunk_k[i] = 8 * c;
     if (row < BM) {
       const int64_t m = min(m0 + row, M - 1);
@@ -165,20 +170,20 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
       src[i] = G.w + n * G.ldw + 8 * c;
     }
   }
-  // Issue stage kt's loads into ring slot `slot`. In the 32-wide tail stage
-  // (k % 64 == 32) chunks past k re-read a valid chunk; nothing multiplies
+  // Issue stage kt's loads into ring slot `slot`. In a partial tail stage
+  // (k % BK != 0) chunks past k re-read a valid chunk; nothing multiplies
   // them.
   // This workgroup's k stages: [kb, kb + nk) of the product's nk_all, all
   // of them unless k is split over `parts` workgroups.
-  const int nk_all = (K + 63) / 64;
+  const int nk_all = (K + BK - 1) / BK;
   const int spp = kSplit ? (nk_all + args.parts - 1) / args.parts : nk_all;
   const int kb = kSplit ? min(part * spp, nk_all) : 0;
   const int nk = kSplit ? min(nk_all, kb + spp) - kb : nk_all;
-  const bool has_tail = (K & 63) && kb + nk == nk_all;  // the 32-wide tail stage is ours
+  const bool has_tail = (K % BK) && kb + nk == nk_all;  // the partial stage is ours
   auto issue = [&](int kt, int slot) {
-    const int k0 = (kb + kt) * 64;
+    const int k0 = (kb + kt) * BK;
     const uint32_t base = ring_base + kStageBytes * slot;
-    if (k0 + 64 <= K) {
+    if (k0 + BK <= K) {
 #pragma unroll
       for (int i = 0; i < L; ++i) load_lds16(src[i] + k0, base + 1024u * NW * i);
     } else {
@@ -203,17 +208,18 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
     constexpr int kSteps = decltype(steps_c)::value;
     constexpr bool kIssue = decltype(issue_c)::value;
     constexpr int kMfma = kSteps * TM * TN;
-    const Stage<BM, BN>& st = ring[kt % S];
+    const Stage<BM, BN, KC>& st = ring[kt % S];
     // (kt counts this workgroup's stages; k offsets add kb)
     uint4 af[kSteps][TM], bf[kSteps][TN];
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
 #pragma unroll
-      for (int a = 0; a < TM; ++a) af[s][a] = st.c[swz(wm * WM + a * 16 + li, 4 * s + lg)];
+      for (int a = 0; a < TM; ++a) af[s][a] = st.c[swz<KC>(wm * WM + a * 16 + li, 4 * s + lg)];
 #pragma unroll
-      for (int b = 0; b < TN; ++b) bf[s][b] = st.c[swz(BM + wn * WN + b * 16 + li, 4 * s + lg)];
+      for (int b = 0; b < TN; ++b)
+        bf[s][b] = st.c[swz<KC>(BM + wn * WN + b * 16 + li, 4 * s + lg)];
     }
-    const int k1 = (kb + kt + S - 1) * 64;
+    const int k1 = (kb + kt + S - 1) * BK;
     const uint32_t base = ring_base + kStageBytes * ((kt + S - 1) % S);
     int issued = 0;
 #pragma unroll
@@ -248,8 +254,8 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
   // until only the loads of stages kt+1 .. min(kt+S-2, nk-1) are pending and
   // its LDS reads are done; one barrier publishes stage kt to every wave and
   // retires slot (kt-1) % S, which receives stage kt + S - 1 while stage kt
-  // is multiplied. Only the last stage can be a 32-wide tail, and nothing is
-  // issued after it.
+  // is multiplied. Only the last stage can be partial (32, 64 or 96 wide),
+  // and nothing is issued after it.
   static_assert(S >= 2 && S <= 8, "wait ladder covers rings of 2..8 stages");
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)
@@ -259,14 +265,22 @@ __global__ __launch_bounds__(64 * GM * GN) void proj_kernel(const ProjArgs args)
     if (kt + S - 1 < nk) {
       if (kt + S - 1 == nk - 1 && has_tail) {
         issue(kt + S - 1, (kt + S - 1) % S);  // the tail stage's clamped loads
-        stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
+        stage(kt, std::integral_constant<int, kStepsFull>{}, std::false_type{});
       } else {
-        stage(kt, std::integral_constant<int, 2>{}, std::true_type{});
+        stage(kt, std::integral_constant<int, kStepsFull>{}, std::true_type{});
       }
-    } else if ((kb + kt) * 64 + 64 <= K) {
-      stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
+    } else if ((kb + kt) * BK + BK <= K) {
+      stage(kt, std::integral_constant<int, kStepsFull>{}, std::false_type{});
     } else {
-      stage(kt, std::integral_constant<int, 1>{}, std::false_type{});
+      const int steps = (K - (kb + kt) * BK) / 32;  // 1 .. kStepsFull - 1
+      if (steps == 1) {
+        stage(kt, std::integral_constant<int, 1>{}, std::false_type{});
+      } else if constexpr (kStepsFull > 2) {
+        if (steps == 2)
+          stage(kt, std::integral_constant<int, 2>{}, std::false_type{});
+        else
+          stage(kt, std::integral_constant<int, 3>{}, std::false_type{});
+      }
     }
   }
 
@@ -328,7 +342,7 @@ struct TileShape {
 
 // Tile shapes, largest first (fewest re-reads of x and w); measured on the
 // MI355X inside HIP graphs.
-constexpr TileShape kShapes[] = {{64, 64}, {64, 32}, {32, 32}};
+constexpr TileShape kShapes[] = {{64, 64}, {32, 32}};
 
 int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) {
   int64_t tiles = 0;
@@ -337,7 +351,7 @@ int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) 
   return tiles;
 }
 
-template <int BM, int BN, int S, int GM = 2, int GN = 2>
+template <int BM, int BN, int S, int GM = 2, int GN = 2, int BK = 64>
 int launch(int64_t m, const wkv7_proj_group* gs, int ng, int parts, float* ws, hipStream_t s) {
   ProjArgs args{};
   args.m = m;
@@ -359,9 +373,9 @@ int launch(int64_t m, const wkv7_proj_group* gs, int ng, int parts, float* ws, h
   args.xcd_span = int32_t((end + kXcds - 1) / kXcds);
   const unsigned grid = unsigned(args.xcd_span) * kXcds;
   if (parts == 1) {
-    proj_kernel<BM, BN, S, GM, GN, false><<<grid, 64 * GM * GN, 0, s>>>(args);
+    proj_kernel<BM, BN, S, GM, GN, BK, false><<<grid, 64 * GM * GN, 0, s>>>(args);
   } else {
-    proj_kernel<BM, BN, S, GM, GN, true><<<grid, 64 * GM * GN, 0, s>>>(args);
+    proj_kernel<BM, BN, S, GM, GN, BK, true><<<grid, 64 * GM * GN, 0, s>>>(args);
     const int rc = launch_status();
     if (rc != WKV7_OK) return rc;
     const int64_t blocks = (elems + 255) / 256;
@@ -380,18 +394,14 @@ struct Plan {
 };
 
 Plan make_plan(int64_t m, const wkv7_proj_group* gs, int ng, int cus) {
-  // 64 x 64 tiles (8 waves) when they give every compute unit about two
-  // workgroups (one waits at its stage barrier while the other computes),
-  // else 64 x 32 tiles when they cover most units, else 32 x 32 tiles with
-  // a deeper ring.
-  Plan p{2, 1, 0};
-  int64_t tiles = count_tiles(m, gs, ng, kShapes[2]);
+  // 64 x 64 tiles (8 waves, 2-stage ring of 128-wide k stages) when they
+  // give every compute unit about 1.5 workgroups or more; else 32 x 32 tiles
+  // (4 waves, 4-stage ring).
+  Plan p{1, 1, 0};
+  int64_t tiles = count_tiles(m, gs, ng, kShapes[1]);
   if (count_tiles(m, gs, ng, kShapes[0]) * 2 >= int64_t(cus) * 3) {
     p.shape = 0;
     tiles = count_tiles(m, gs, ng, kShapes[0]);
-  } else if (count_tiles(m, gs, ng, kShapes[1]) * 5 >= int64_t(cus) * 4) {
-    p.shape = 1;
-    tiles = count_tiles(m, gs, ng, kShapes[1]);
   }
   // At most one workgroup per two units and long k: split k so that about two
   // workgroups per unit each walk at least 8 stages. (With more tiles the
@@ -474,9 +484,6 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
     p.parts = 1;
   float* ws = static_cast<float*>(workspace);
   hipStream_t s = as_stream(stream);
-  switch (p.shape) {
-    case 0: return launch<64, 64, 4, 2, 4>(m, groups, ngroups, p.parts, ws, s);
-    case 1: return launch<64, 32, 4, 2, 2>(m, groups, ngroups, p.parts, ws, s);
-    default: return launch<32, 32, 8, 2, 2>(m, groups, ngroups, p.parts, ws, s);
-  }
+  if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
 }
