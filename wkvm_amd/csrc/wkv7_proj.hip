@@ -14,14 +14,17 @@
 // A[li][8lg .. 8lg+7] of a 32-wide k block, B lane holds B[8lg .. 8lg+7][li],
 // the accumulator holds D[4lg .. 4lg+3][li]. With x rows and w rows both
 // k-contiguous, every operand register is one 16-byte chunk of one row.
-// k advances 64 per stage through a ring of S LDS stages whose 128-byte rows
-// hold 8 chunks, chunk c of row r at slot c ^ (r & 7), so the 16 rows a
-// fragment read touches spread over the banks. Stages are filled by direct
-// global -> LDS loads (no register staging) issued S - 1 stages ahead and
-// spread between the MFMAs of the stage being multiplied. One barrier per
-// stage. Rows past m and columns past n load a clamped (valid) row and are
-// not stored. Tiles are dealt to the XCDs in contiguous runs so that each
-// XCD's L2 keeps the x rows it re-reads.
+// k advances BK (64 or 128) per stage through a ring of S LDS stages whose
+// rows hold KC = BK / 8 chunks of 16 bytes, chunk c of row r at slot
+// c ^ (r & (KC - 1)), so the 16 rows a fragment read touches spread over the
+// banks. Stages are filled by direct global -> LDS loads (no register
+// staging) issued S - 1 stages ahead and spread between the MFMAs of the
+// stage being multiplied. One barrier per stage. Rows past m and columns past
+// n load a clamped (valid) row and are not stored. Tiles are dealt to the
+// XCDs in contiguous runs so that each XCD's L2 keeps the x rows it
+// re-reads. With few tiles and long k, k can be split over several
+// workgroups per tile (fp32 partials in a caller-provided workspace, summed
+// in part order by proj_reduce_kernel).
 #include <algorithm>
 #include <type_traits>
 
@@ -423,9 +426,6 @@ Plan make_plan(int64_t m, const wkv7_proj_group* gs, int ng, int cus) {
   }
   return p;
 }
-
-int validate(int64_t m, const wkv7_proj_group* groups, int32_t ngroups);
-int device_cus(int* cus);
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
