@@ -42,7 +42,13 @@ __device__ __forceinline__ float el(const Bf8& v, int e) {
 
 // Sequence of token t: the largest s with cu[s] <= t (empty sequences have
 // cu[s] == cu[s+1] and are skipped by taking the largest such s).
+// The last sequence s with cu[s] <= t (the one holding token t when t is
+// inside a sequence). Decode batches have one token per sequence, so s = t is
+// tried first: one load pair instead of a binary search of dependent loads,
+// which dominated the latency of a small launch.
 __device__ __forceinline__ int seq_of(const int32_t* cu, int nseq, int64_t t) {
+  const int g = int(t < int64_t(nseq - 1) ? t : int64_t(nseq - 1));
+  if (int64_t(cu[g]) <= t && t < int64_t(cu[g + 1])) return g;
   int lo = 0, hi = nseq - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
