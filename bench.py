@@ -57,8 +57,8 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("fork_decode_7b", "mixed_ragged", "decode_graph",
-                                       "state_store", "time_mix"),
+    ap.add_argument("--only", choices=("fla_decode", "fork_decode_7b", "mixed_ragged",
+                                       "decode_graph", "state_store", "time_mix"),
                     help="run just this extra section and print its result as JSON (for "
                          "rocprofv3 runs; not the benchmark line)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -84,10 +84,9 @@ class Launcher:
         if rc:
             self.check(rc, "wkv7_decode_slots")
 
-    def prefill(self, pool, rows, H, ids, cu, nseq, T, xs, y, zero_init, ws=None, ws_bytes=0,
-                order=None):
+    def prefill(self, pool, rows, H, ids, cu, nseq, T, xs, y, zero_init, order=None):
         rc = self.lib.wkv7_prefill_varlen(pool, rows, H, ids, cu, order, nseq, T, *xs, y, 0,
-                                          zero_init, 1.0, ws, ws_bytes, self.stream)
+                                          zero_init, 1.0, self.stream)
         if rc:
             self.check(rc, "wkv7_prefill_varlen")
 
@@ -187,6 +186,56 @@ def bench_decode(torch, dev, args, launcher):
     return res
 
 
+def bench_fla_decode(torch, dev, args):
+    """Config 1 through fla's wkv-op signature (the reference model layer's
+    decode call, wkvm/models/rwkv7.py:108-111): per layer,
+    ``o, final = fused_recurrent_rwkv7(r, w, k, v, a, b, initial_state=state_l,
+    output_final_state=True)`` on dense [256, H, 64, 64] states, and the
+    caller keeps ``final`` as the layer's next state (as fla's Cache does).
+    The call runs the decode kernel out of place: each state is read once
+    and written once. Timed with the Python wrapper's per-call validation in
+    the loop (events around each 24-layer step) and per kernel launch."""
+    from wkvm_amd import ops, synthetic
+
+    L, H, B, NSETS = 24, 32, 256, 4
+    gdev = synthetic.make_generator(args.seed + 21, dev)
+    states = [torch.empty((B, H, 64, 64), dtype=torch.float32, device=dev).normal_(
+        0.0, 0.1, generator=gdev) for _ in range(L)]
+    sets = [[synthetic.order(synthetic.wkv7_vectors((B, 1, H, 64), gdev)) for _ in range(NSETS)]
+            for _ in range(L)]
+
+    def step(i):
+        for l in range(L):
+            _, states[l] = ops.fused_recurrent_rwkv7(*sets[l][i % NSETS],
+                                                      initial_state=states[l])
+
+    for i in range(3):
+        step(i)
+    torch.cuda.synchronize()
+    steps = max(10, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    layer_bytes = B * slot_layer_bytes(H)
+    res = {
+        "slot_steps_per_s": B / (ms * 1e-3),
+        "ms_per_step": ms,
+        "hbm_gbps": L * layer_bytes / (ms * 1e-3) / 1e9,
+        "hbm_frac": L * layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "steps": steps,
+        "state_bytes_per_layer": 2 * B * H * HEAD_STATE_B,
+    }
+    log(f"fla decode cfg1: {ms:.3f} ms/step ({res['slot_steps_per_s']:.0f} slot-steps/s), "
+        f"{res['hbm_gbps']:.0f} GB/s = {res['hbm_frac']:.3f} of peak")
+    del states, sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_prefill(torch, dev, args, launcher):
     """Config 2: 1.5B shape, 8 sequences x 4096 tokens, zero initial state,
     final states into 8 seeded slots; per-layer launch timing over 3 distinct
@@ -202,13 +251,9 @@ def bench_prefill(torch, dev, args, launcher):
     pools = [torch.zeros((S + 1, H, 64, 64), dtype=torch.float32, device=dev) for _ in range(NL)]
     xs = [synthetic.order(synthetic.wkv7_vectors((nseq * T, H, 64), gdev)) for _ in range(NL)]
     ys = [torch.empty((nseq * T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(NL)]
-    ws_bytes = ops.prefill_workspace_bytes(H, nseq, nseq * T)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    ws_ptr = ws.data_ptr() if ws_bytes else None
-
     def run(l):
         launcher.prefill(pools[l].data_ptr(), S + 1, H, ids_t.data_ptr(), cu_t.data_ptr(), nseq,
-                         nseq * T, ptrs(xs[l]), ys[l].data_ptr(), 1, ws_ptr, ws_bytes)
+                         nseq * T, ptrs(xs[l]), ys[l].data_ptr(), 1)
 
     for i in range(2):
         run(i % NL)
@@ -235,12 +280,11 @@ def bench_prefill(torch, dev, args, launcher):
         "mfma_util": flops_layer / (ms * 1e-3) / (BF16_DENSE_PEAK_TFLOPS * 1e12),
         "algorithmic_bytes_per_layer": bytes_layer,
         "algorithmic_flops_per_layer": flops_layer,
-        "workspace_bytes": ws_bytes,
         "tokens_per_s_24_layers": tokens / (ms * 1e-3) / 24,
     }
     log(f"prefill cfg2: {res['tokens_per_s_per_layer']:.3e} tok/s/layer, {ms:.3f} ms/layer, "
         f"{res['hbm_gbps']:.0f} GB/s, MFMA {100 * res['mfma_util']:.2f} %")
-    del pools, xs, ys, ws
+    del pools, xs, ys
     torch.cuda.empty_cache()
     res["one_sequence"] = bench_prefill_one_sequence(torch, dev, args)
     return res
@@ -382,9 +426,6 @@ def bench_mixed(torch, dev, args, launcher):
     px = [synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev)) for _ in range(2)]
     dy = torch.empty((ND, H, 64), dtype=torch.bfloat16, device=dev)
     py = torch.empty((T, H, 64), dtype=torch.bfloat16, device=dev)
-    ws_bytes = ops.prefill_workspace_bytes(H, NP, T)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    ws_ptr = ws.data_ptr() if ws_bytes else None
 
     side = torch.cuda.Stream(dev)  # default priority
     main = torch.cuda.current_stream(dev)
@@ -400,7 +441,7 @@ def bench_mixed(torch, dev, args, launcher):
                 launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(),
                                 dec_order.data_ptr(), ND, ptrs(dx[l]), dy.data_ptr())
             launcher.prefill(wkv[l].data_ptr(), S + 1, H, pre_t.data_ptr(), cu_t.data_ptr(), NP, T,
-                             ptrs(px[l % 2]), py.data_ptr(), 1, ws_ptr, ws_bytes, order)
+                             ptrs(px[l % 2]), py.data_ptr(), 1, order)
             if decode and concurrent:
                 launcher.decode(wkv[l].data_ptr(), S + 1, H, dec_t.data_ptr(),
                                 dec_order.data_ptr(), ND, ptrs(dx[l]), dy.data_ptr(),
@@ -439,7 +480,7 @@ def bench_mixed(torch, dev, args, launcher):
         f"{ms_serial:.2f} ms on one stream), {T} prefill tokens + {ND} decodes, "
         f"{res['hbm_gbps']:.0f} GB/s; prefill alone {pre_lpt:.2f} ms longest-first, "
         f"{pre_idx:.2f} ms index order")
-    del wkv, dx, px, dy, py, ws
+    del wkv, dx, px, dy, py
     torch.cuda.empty_cache()
     return res
 
@@ -684,17 +725,31 @@ def bench_time_mix(torch, dev, args):
     return res
 
 
+def cpu_model() -> str | None:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(args):
-    """fp32 C port (oracle/) on this host: config-1 decode (24 layers x 256
-    slots of a 512-slot pool) for as many steps as fit ~10 s, at least one;
-    then config-2 prefill (one layer, 8 sequences) for ~5 s."""
+    """fp32 C port (oracle/) on this host, OpenMP over every core in this
+    process's affinity set: config-1 decode (24 layers x 256 slots of a
+    512-slot pool) for as many steps as fit ~10 s, at least one; then config-2
+    prefill (one layer, 8 sequences) for ~5 s."""
     import numpy as np
     import torch
 
     import oracle as O
     from wkvm_amd import synthetic
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    affinity = len(os.sched_getaffinity(0))
+    threads = affinity  # every core this process may run on
     O.set_threads(threads)
     L, H, S, B = 24, 32, 512, 256
     gen = synthetic.make_generator(args.seed)
@@ -717,11 +772,16 @@ def cpu_baseline(args):
         "value": B * steps / el,
         "unit": "slot-steps/s",
         "cores": threads,
+        "threads": threads,
+        "nproc": os.cpu_count(),
+        "affinity_cores": affinity,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{steps} config-1 decode steps (24 layers x 256 slots, H=32), fp32 C port "
                   f"with OpenMP, {el:.1f} s",
     }
-    log(f"cpu baseline: {res['value']:.1f} slot-steps/s on {threads} threads ({steps} steps)")
+    log(f"cpu baseline: {res['value']:.1f} slot-steps/s on {threads} threads ({steps} steps; "
+        f"nproc {res['nproc']}, affinity {affinity}, {res['cpu_model']})")
     del pool
     # config-2 prefill (one layer): 8 sequences from zero state, 512-token
     # slices of the 4096-token rows, repeated for ~5 s
@@ -832,7 +892,8 @@ def main() -> int:
         pmc_probe(torch, dev, args, launcher)
         return 0
     if args.only:
-        fn = {"fork_decode_7b": lambda: bench_fork_decode_7b(torch, dev, args, launcher),
+        fn = {"fla_decode": lambda: bench_fla_decode(torch, dev, args),
+              "fork_decode_7b": lambda: bench_fork_decode_7b(torch, dev, args, launcher),
               "mixed_ragged": lambda: bench_mixed(torch, dev, args, launcher),
               "decode_graph": lambda: bench_decode_graph(torch, dev, args),
               "state_store": lambda: bench_store(torch, dev, args),
@@ -843,6 +904,7 @@ def main() -> int:
     pre = bench_prefill(torch, dev, args, launcher)
     extra = {}
     if not args.no_extra:
+        extra["fla_decode"] = bench_fla_decode(torch, dev, args)
         extra["fork_decode_7b"] = bench_fork_decode_7b(torch, dev, args, launcher)
         extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)
         extra["decode_graph"] = bench_decode_graph(torch, dev, args)

@@ -29,7 +29,8 @@
  *        h[j][i] = exp(w[j]) h[j][i] + b[j] p_i + k[j] v[i]
  *        y[i]    = sum_j (scale r[j]) h[j][i]
  *  - Slot ids are int32 in device memory. A kernel never touches memory
- *    outside [0, num_rows): rows whose id is out of range are skipped. Host
+ *    outside [0, num_rows): rows whose id is out of range are skipped (the
+ *    decode entry points write zeros into such a row's outputs). Host
  *    wrappers validate ids before launch and raise instead.
  *  - Return value: 0 on success, a negative WKV7_ERR_* code for rejected
  *    arguments (nothing is enqueued), or a positive hipError_t from the launch.
@@ -46,7 +47,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 8
+#define WKV7_ABI_VERSION 9
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -83,13 +84,46 @@ const char *wkv7_strerror(int code);
  *              neighbouring slot regions and raise bandwidth when slots are
  *              scattered through the pool. Entries outside [0, B) are skipped.
  *   r..b       [B, H, 64] bf16
- *   y          [B, H, 64], dtype per y_dtype (WKV7_Y_BF16 | WKV7_Y_F32)
+ *   y          [B, H, 64], dtype per y_dtype (WKV7_Y_BF16 | WKV7_Y_F32); a
+ *              row whose slot id is outside [0, num_rows) gets y = 0 and its
+ *              state is not touched
  */
 int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
                       const int32_t *slot_ids, const int32_t *row_order, int32_t B,
                       const uint16_t *r, const uint16_t *w, const uint16_t *k,
                       const uint16_t *v, const uint16_t *a, const uint16_t *b,
                       void *y, int32_t y_dtype, float scale, void *stream);
+
+/*
+ * One decode step (one token per row) with the state read from one tensor and
+ * written to another: row b reads state_in[in_ids[b]] and writes
+ * state_out[out_ids[b]] (both [rows, H, 64, 64] fp32). The arithmetic is
+ * wkv7_decode_slots'; with state_in == state_out and in_ids == out_ids it is
+ * that call.
+ *
+ * Replaces fla's recurrent WKV7 op at seq_len 1 as the reference's model
+ * layer calls it (dispatched for seq_len < 64, wkvm/models/rwkv7.py:108-111;
+ * reached from RWKV7Runner.decode_step, wkvm/runner/runner.py:74-76):
+ * fused_recurrent_rwkv7(r, w, k, v, a, b, initial_state=, output_final_state=)
+ * reads initial_state and returns a new final_state tensor.
+ *
+ *   state_in   NULL = zero initial state (fla's initial_state=None)
+ *   in_ids     [B] int32 (device), or NULL: row b reads state row b
+ *   state_out  NULL = the new state is not written (output_final_state=False)
+ *   out_ids    [B] int32 (device), or NULL: row b writes state row b; must be
+ *              distinct, and no row may write a state row another row reads
+ *   in_rows, out_rows   rows of each tensor (at least B where its ids are NULL,
+ *              else WKV7_ERR_SHAPE); ids outside [0, rows) give y = 0 and no
+ *              state write for that row
+ *   H, row_order, B, r..b, y, y_dtype, scale   as wkv7_decode_slots
+ * Ids without their tensor are WKV7_ERR_ARG.
+ */
+int wkv7_decode_into(const float *state_in, int64_t in_rows, const int32_t *in_ids,
+                     float *state_out, int64_t out_rows, const int32_t *out_ids,
+                     int32_t H, const int32_t *row_order, int32_t B,
+                     const uint16_t *r, const uint16_t *w, const uint16_t *k,
+                     const uint16_t *v, const uint16_t *a, const uint16_t *b,
+                     void *y, int32_t y_dtype, float scale, void *stream);
 
 /*
  * Chunked prefill of nseq ragged sequences of one layer; each sequence starts
@@ -114,9 +148,6 @@ int wkv7_decode_slots(float *wkv_layer, int64_t num_rows, int32_t H,
  *                 depend on it
  *   r..b          [total_tokens, H, 64] bf16, 16-byte aligned (else WKV7_ERR_SHAPE)
  *   y             [total_tokens, H, 64], dtype per y_dtype
- *   workspace     device scratch of at least
- *                 wkv7_prefill_workspace_bytes(H, nseq, total_tokens) bytes
- *                 (may be NULL when that size is 0)
  *
  * Decay range: the chunked form scales operands by exp(+-G) with G a sum of
  * up to 16 consecutive log-decays, so every w must be >= -5 (exp(80) is
@@ -129,10 +160,7 @@ int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
                         const uint16_t *r, const uint16_t *w, const uint16_t *k,
                         const uint16_t *v, const uint16_t *a, const uint16_t *b,
                         void *y, int32_t y_dtype, int32_t zero_init, float scale,
-                        void *workspace, size_t workspace_bytes, void *stream);
-
-/* Scratch bytes wkv7_prefill_varlen needs for this problem size. */
-size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t total_tokens);
+                        void *stream);
 
 /* Run flags of wkv7_prefill_runs. */
 #define WKV7_RUN_INIT_ZERO 1      /* start from zero state */

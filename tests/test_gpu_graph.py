@@ -50,6 +50,35 @@ def test_graph_replays_match_eager(dev, y_dtype):
         del scratch
 
 
+def test_graph_replays_match_oracle(dev):
+    """DecodeGraph replays (the role of the reference's GraphedDecode,
+    experiments/m2_engine_bench.py:44-131) at the 1.5B head count: three
+    replays with different slot batches, every layer's state and y checked
+    against the float64 oracle from the state before the replay."""
+    import numpy as np
+
+    import oracle as O
+    from tests import util as U
+
+    layout, _, graphed = _banks(dev, L=2, H=32, S=96, seed=21)
+    L, H, B = layout.n_layer, layout.num_heads, 48
+    dg = DecodeGraph(graphed, B, out_dtype=torch.float32)
+    gcpu = synthetic.make_generator(22)
+    for step in range(3):
+        slots = synthetic.active_slots(graphed.num_slots, B, gcpu)
+        vecs = [synthetic.wkv7_vectors((B, H, 64), gcpu) for _ in range(L)]
+        before = graphed.wkv.cpu().numpy()
+        y = dg.step(slots, [[v[n].to(dev) for n in "rwkvab"] for v in vecs])
+        torch.cuda.synchronize()
+        for layer in range(L):
+            y_ref, h_ref = O.scan_bf16(np.arange(B + 1), *U.vec_bits(vecs[layer]),
+                                       pool=before[layer], slot_ids=slots)
+            assert U.normwise_max(U.f64(graphed.wkv[layer, slots]), h_ref) <= 1e-5, step
+            assert U.normwise_max(U.f64(y[layer]), y_ref, tile_dims=1) <= 1e-5, step
+        idle = sorted(set(range(graphed.num_slots + 1)) - set(slots))
+        assert np.array_equal(graphed.wkv[:, idle].cpu().numpy(), before[:, idle])
+
+
 def test_graph_rejects_wrong_batch(dev):
     _, _, graphed = _banks(dev)
     dg = DecodeGraph(graphed, 3)

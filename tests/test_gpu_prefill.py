@@ -418,3 +418,31 @@ def test_fla_signature_long_single_sequence_runs_segmented(dev):
                                    slot_ids=None if init is None else [0])
         assert U.rel_l2(U.f64(hT), h_ref) <= REL_L2
         assert U.rel_l2(U.f64(o[0]), O.round_f64_to_bf16(y_ref)) <= REL_L2
+
+
+@pytest.mark.parametrize("chunk,segments", [(512, None), (4096, "auto")])
+def test_runner_prefill_matches_oracle(dev, chunk, segments):
+    """WKV7Runner.prefill (wkvm/runner/runner.py:41-63): one 4,096-token
+    request at the 1.5B head count, two layers, from a non-zero slot state,
+    in 512-token chunks re-entering through the slot (and in one 4,096-token
+    chunk that runs segmented); every layer's y and the final slot state
+    against the float64 oracle, the pad row and the other slots untouched."""
+    Lr, H, T = 2, 32, 4096
+    lay = RWKV7StateLayout(n_layer=Lr, hidden_size=H * 64, num_heads=H, head_dim=64,
+                           head_v_dim=64, dtype=torch.bfloat16)
+    bank = RWKV7StateBank(lay, num_slots=4, device=dev)
+    gen = synthetic.make_generator(421)
+    bank.wkv[:, 1:] = synthetic.initial_states((Lr, 4, H, 64, 64), gen).to(dev)
+    before = bank.wkv.cpu()
+    vecs = [synthetic.wkv7_vectors((T, H, 64), gen) for _ in range(Lr)]
+    run = WKV7Runner(bank, prefill_chunk=chunk, prefill_segments=segments)
+    ys = run.prefill([[v[n].to(dev) for n in "rwkvab"] for v in vecs], {"wkv": 3, "shift": 3})
+    torch.cuda.synchronize()
+    for layer in range(Lr):
+        y_ref, h_ref = O.scan_bf16(np.array([0, T]), *U.vec_bits(vecs[layer]),
+                                   pool=before[layer].numpy(), slot_ids=[3])
+        eh = U.rel_l2(U.f64(bank.wkv[layer, 3]), h_ref[0])
+        ey = U.rel_l2(U.f64(ys[layer]), O.round_f64_to_bf16(y_ref))
+        print(f"layer {layer}: state rel L2 {eh:.2e}, y {ey:.2e}")
+        assert eh <= REL_L2 and ey <= REL_L2
+    assert torch.equal(bank.wkv[:, [0, 1, 2, 4]].cpu(), before[:, [0, 1, 2, 4]])

@@ -35,7 +35,7 @@ def test_save_is_the_slot_view(dev, tmp_path):
     bank = _bank(dev)
     st = StateStore(bank, tmp_path)
     h = st.save("s", {"wkv": 3, "shift": 4}, 5, [1, 2, 3, 4, 5, 6])
-    t = st._tensors(h)
+    t = st.host_tensors(h)
     assert t["wkv"].is_pinned() and t["shift"].is_pinned()
     assert torch.equal(t["wkv"], bank.wkv[:, 3].cpu())
     assert torch.equal(t["shift"], bank.shift[:, :, 4].cpu())
@@ -47,7 +47,7 @@ def test_load_writes_only_the_target_slot(dev, tmp_path):
     bank = _bank(dev)
     st = StateStore(bank, tmp_path)
     h = st.save("s", {"wkv": 2, "shift": 2}, 0, [0])
-    saved = {k: v.clone() for k, v in st._tensors(h).items()}
+    saved = {k: v.clone() for k, v in st.host_tensors(h).items()}
     before_w, before_s = bank.wkv.clone(), bank.shift.clone()
     st.load(h, {"wkv": 5, "shift": 1})
     assert torch.equal(bank.wkv[:, 5].cpu(), saved["wkv"])
@@ -99,7 +99,7 @@ def test_rejected_load_moves_nothing(dev, tmp_path):
     with pytest.raises(FingerprintMismatch):
         st.load(h, {"wkv": 2, "shift": 2})
     with pytest.raises(ValueError):
-        ops.slot_from_host(bank.wkv, bank.num_slots + 1, 1, st._tensors(h)["wkv"])
+        ops.slot_from_host(bank.wkv, bank.num_slots + 1, 1, st.host_tensors(h)["wkv"])
     torch.cuda.synchronize()
     assert torch.equal(bank.wkv, before_w) and torch.equal(bank.shift, before_s)
 

@@ -68,7 +68,18 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == 8
+    assert lib.wkv7_abi_version() == _lib.WKV7_ABI_VERSION == 9
+
+
+def test_a_library_of_another_abi_version_is_refused(monkeypatch):
+    """A stale libwkv7.so (built from other sources) would be called with the
+    wrong argument lists; load() compares its version with the binding's and
+    raises with a rebuild hint instead."""
+    _lib.load()
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "WKV7_ABI_VERSION", _lib.WKV7_ABI_VERSION - 1)
+    with pytest.raises(RuntimeError, match="rebuild"):
+        _lib.load()
 
 
 def test_abi_rejects_bad_arguments_before_any_launch():
@@ -82,11 +93,25 @@ def test_abi_rejects_bad_arguments_before_any_launch():
     assert lib.wkv7_decode_slots(None, 5, 2, dummy, None, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
     assert lib.wkv7_decode_slots(dummy, 5, 0, dummy, None, 1, *six, dummy, 0, 1.0, None) == _lib.WKV7_ERR_ARG
     assert lib.wkv7_decode_slots(dummy, 5, 2, dummy, None, 0, *six, dummy, 0, 1.0, None) == _lib.WKV7_OK
+    # out-of-place decode: ids without their tensor, too few rows without ids,
+    # bad y dtype; zero state in and no state out is a valid launch shape
+    assert lib.wkv7_decode_into(None, 0, dummy, dummy, 4, None, 2, None, 1, *six, dummy, 0, 1.0,
+                                None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_into(dummy, 4, None, None, 0, dummy, 2, None, 1, *six, dummy, 0, 1.0,
+                                None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_into(dummy, 2, None, dummy, 4, None, 2, None, 3, *six, dummy, 0, 1.0,
+                                None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_decode_into(None, 0, None, dummy, 2, None, 2, None, 3, *six, dummy, 0, 1.0,
+                                None) == _lib.WKV7_ERR_SHAPE
+    assert lib.wkv7_decode_into(None, 0, None, None, 0, None, 2, None, 3, *six, dummy, 9, 1.0,
+                                None) == _lib.WKV7_ERR_ARG
+    assert lib.wkv7_decode_into(None, 0, None, None, 0, None, 2, None, 0, *six, dummy, 0, 1.0,
+                                None) == _lib.WKV7_OK
     # prefill: negative sizes, missing cu_seqlens
     assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, dummy, None, -1, 0, *six, dummy, 0, 0,
-                                   1.0, None, 0, None) == _lib.WKV7_ERR_ARG
+                                   1.0, None) == _lib.WKV7_ERR_ARG
     assert lib.wkv7_prefill_varlen(dummy, 5, 2, dummy, None, None, 1, 4, *six, dummy, 0, 0,
-                                   1.0, None, 0, None) == _lib.WKV7_ERR_ARG
+                                   1.0, None) == _lib.WKV7_ERR_ARG
     # slot copy: negative count, null src, row wider than the slot stride
     assert lib.wkv7_slot_copy(dummy, 0, 64, 4, None, dummy, 0, 64, 4, None, 1, 64, -1,
                               None) == _lib.WKV7_ERR_ARG

@@ -260,3 +260,17 @@ def test_scan_bf16_variant_equals_f64_variant():
     y3, h3 = O.scan_bf16(cu, *bitsd)
     y4, h4 = O.scan_f64(cu, *f64)
     assert np.array_equal(y3, y4) and np.array_equal(h3, h4)
+
+
+def test_bf16_output_bar_helper():
+    """The bf16-output bar of the GPU tests: an exactly rounded output sits at
+    half its bar, and two planted ulps on one element fail it."""
+    from tests import util as U
+
+    rng = np.random.default_rng(0)
+    ref = rng.standard_normal((100, 64)) * 5
+    bits = O.f32_to_bf16_bits(ref.astype(np.float32))
+    assert U.bf16_y_excess(bits, ref) <= 0.5 + 1e-9
+    bad = bits.copy()
+    bad[3, 5] += 2
+    assert U.bf16_y_excess(bad, ref) > 1

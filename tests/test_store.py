@@ -40,10 +40,7 @@ def _tensors(bank, seed):
 
 
 def _put(store, name, tensors, tokens=(1, 2, 3)):
-    rec = StateRecord(name=name, version=store._next_version(name),
-                      fingerprint=store.fingerprint, num_computed_tokens=len(tokens) - 1,
-                      token_ids=tuple(tokens))
-    return store._add(rec, tensors)
+    return store.save_host(name, tensors, len(tokens) - 1, list(tokens))
 
 
 def test_fingerprint_is_the_reference_key_hash(tmp_path):
@@ -60,7 +57,7 @@ def test_versions_lineage_and_index_rebuild(tmp_path):
     assert (h0, h1) == ("sess@0", "sess@1")
     child = st.fork(h1, "kid")
     assert child == "kid@0" and st.get(child).parent == h1
-    assert st._tensors(child) is st._tensors(h1)  # fork moves no bytes
+    assert st.host_tensors(child) is st.host_tensors(h1)  # fork moves no bytes
     mut = st.mutate(h0, "decay", {"alpha": 0.5})
     rec = st.get(mut)
     assert (mut, rec.parent, rec.rule, rec.rule_params) == ("sess@2", h0, "decay", {"alpha": 0.5})
@@ -73,10 +70,10 @@ def test_versions_lineage_and_index_rebuild(tmp_path):
     st2 = StateStore(bank, tmp_path)
     assert [r.handle for r in st2.list()] == [child, h0, h1, mut]
     assert st2.get(mut) == rec
-    for k, v in st._tensors(h1).items():
-        assert torch.equal(st2._tensors(h1)[k], v)
+    for k, v in st.host_tensors(h1).items():
+        assert torch.equal(st2.host_tensors(h1)[k], v)
     with pytest.raises(KeyError):
-        st2._tensors(h0)  # WARM-only record of the old process
+        st2.host_tensors(h0)  # WARM-only record of the old process
     st2.delete(h1)
     assert not (tmp_path / "sess_v1.safetensors").exists()
     assert h1 not in json.loads((tmp_path / "index.json").read_text())
@@ -96,7 +93,7 @@ def test_cold_file_format(tmp_path):
     assert data["shift"].dtype == torch.bfloat16 and tuple(data["shift"].shape) == (2, 2, 128)
     assert torch.equal(data["wkv"], t["wkv"]) and torch.equal(data["shift"], t["shift"])
     st.evict(h)
-    assert h not in st._warm and torch.equal(st._tensors(h)["wkv"], t["wkv"])
+    assert h not in st._warm and torch.equal(st.host_tensors(h)["wkv"], t["wkv"])
 
 
 def test_decay_rule_arithmetic():
@@ -116,7 +113,7 @@ def test_merge_rule_arithmetic(tmp_path):
     a, b = _tensors(bank, 5), _tensors(bank, 6)
     ha, hb = _put(st, "a", a), _put(st, "b", b)
     hm = st.mutate(ha, "merge", {"other": hb, "weight": 0.3})
-    m = st._tensors(hm)
+    m = st.host_tensors(hm)
     w1, w = np.float32(1.0 - 0.3), np.float32(0.3)
     assert np.array_equal(m["wkv"].numpy(), w1 * a["wkv"].numpy() + w * b["wkv"].numpy())
     sa = O.bf16_bits_to_f64(a["shift"].view(torch.int16).numpy().view(np.uint16)).astype(np.float32)
@@ -139,3 +136,48 @@ def test_errors(tmp_path):
         st.load(h, {"wkv": 1, "shift": 1})
     with pytest.raises(ValueError):  # transfers need a GPU bank
         StateStore(bank, tmp_path / "other").save("y", {"wkv": 1, "shift": 1}, 0, [0])
+
+
+def test_index_rows_and_version_numbers(tmp_path):
+    """Each index row holds exactly the record fields plus ``cold`` (what the
+    reference's reader rebuilds a record from), and an index in that layout
+    written by hand loads here. A name's next version is 1 + its highest
+    live version, so deleting the newest version frees its number."""
+    bank = _bank()
+    st = StateStore(bank, tmp_path)
+    h0 = _put(st, "s", _tensors(bank, 0))
+    h1 = _put(st, "s", _tensors(bank, 1))
+    row = json.loads((tmp_path / "index.json").read_text())[h1]
+    assert set(row) == {f for f in StateRecord.__dataclass_fields__} | {"cold"}
+    st.delete(h1)
+    assert _put(st, "s", _tensors(bank, 2)) == "s@1"
+    st.delete("s@7")  # unknown: no-op
+    assert [r.handle for r in st.list()] == [h0, "s@1"]
+    other = tmp_path / "other"
+    other.mkdir()
+    hand = {"x@3": {"name": "x", "version": 3, "fingerprint": st.fingerprint,
+                    "num_computed_tokens": 2, "token_ids": [7, 8, 9], "parent": None,
+                    "rule": "decay", "rule_params": {"alpha": 0.5}, "cold": False}}
+    (other / "index.json").write_text(json.dumps(hand))
+    st2 = StateStore(bank, other)
+    rec = st2.get("x@3")
+    assert rec.token_ids == (7, 8, 9) and rec.rule_params == {"alpha": 0.5}
+    assert st2._next_version("x") == 4
+
+
+def test_save_host_validation_warm_view_and_shared_forks(tmp_path):
+    bank = _bank()
+    st = StateStore(bank, tmp_path)
+    t = _tensors(bank, 8)
+    with pytest.raises(ValueError):
+        st.save_host("bad", {"wkv": t["wkv"][:1], "shift": t["shift"]}, 0, [0])
+    with pytest.raises(ValueError):
+        st.save_host("bad", {"wkv": t["wkv"].double(), "shift": t["shift"]}, 0, [0])
+    h = _put(st, "p", t)
+    kid = st.fork(h, "kid")
+    assert set(st._warm) == {h, kid}
+    st.evict(h)
+    assert set(st._warm) == {kid}
+    st.delete(h)  # the fork keeps the shared tensors
+    assert torch.equal(st.host_tensors(kid)["wkv"], t["wkv"])
+    assert not (tmp_path / "p_v0.safetensors").exists()

@@ -22,7 +22,7 @@ import torch
 
 from wkvm_amd.layout import RWKV7StateLayout
 from wkvm_amd.state import RWKV7StateBank
-from wkvm_amd.store import StateRecord, StateStore
+from wkvm_amd.store import StateStore
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -32,7 +32,7 @@ CHILD = textwrap.dedent("""
     import torch
     from wkvm_amd.layout import RWKV7StateLayout
     from wkvm_amd.state import RWKV7StateBank
-    from wkvm_amd.store import StateRecord, StateStore
+    from wkvm_amd.store import StateStore
 
     layout = RWKV7StateLayout(n_layer=2, hidden_size=128, num_heads=2, head_dim=64,
                               head_v_dim=64, dtype=torch.bfloat16)
@@ -45,9 +45,7 @@ CHILD = textwrap.dedent("""
                  "shift": torch.randn((2, 2, 128), generator=g).to(torch.bfloat16)}}
 
     def put(name, seed, tokens):
-        rec = StateRecord(name=name, version=st._next_version(name), fingerprint=st.fingerprint,
-                          num_computed_tokens=len(tokens) - 1, token_ids=tuple(tokens))
-        return st._add(rec, tensors(seed))
+        return st.save_host(name, tensors(seed), len(tokens) - 1, tokens)
 
     a = put("sess", 1, [5, 6, 7])
     st.persist(a)
@@ -87,22 +85,20 @@ def test_kill_after_persist_rebuilds_from_index(tmp_path):
     assert [r.handle for r in st.list()] == ["kid@0", "sess@0"]
     assert st.get("kid@0").parent == "sess@0"
     assert st.get("sess@0").token_ids == (5, 6, 7)
-    got, want = st._tensors("sess@0"), _tensors(1)
+    got, want = st.host_tensors("sess@0"), _tensors(1)
     for k in ("wkv", "shift"):
         assert torch.equal(got[k], want[k])
 
 
 def test_kill_mid_index_write_keeps_last_complete_index(tmp_path):
     _run_child(tmp_path, "mid_index")
-    assert (tmp_path / "index.tmp").exists()  # the interrupted write
+    assert (tmp_path / "index.json.partial").exists()  # the interrupted write
     st = StateStore(_bank(), tmp_path)
     assert [r.handle for r in st.list()] == ["kid@0", "sess@0"]  # no "late@0"
     for k in ("wkv", "shift"):
-        assert torch.equal(st._tensors("sess@0")[k], _tensors(1)[k])
+        assert torch.equal(st.host_tensors("sess@0")[k], _tensors(1)[k])
     # the store keeps working after the restart
-    rec = StateRecord(name="late", version=st._next_version("late"), fingerprint=st.fingerprint,
-                      num_computed_tokens=0, token_ids=(1,))
-    st._add(rec, _tensors(2))
+    st.save_host("late", _tensors(2), 0, [1])
     st.persist("late@0")
     assert [r.handle for r in StateStore(_bank(), tmp_path).list()] == ["kid@0", "late@0",
                                                                           "sess@0"]

@@ -44,3 +44,16 @@ def bf16_ulp_distance(y_bits: np.ndarray, ref: np.ndarray) -> np.ndarray:
 
 def vec_bits(vecs: dict[str, torch.Tensor]) -> list[np.ndarray]:
     return [bits(vecs[n]) for n in "rwkvab"]
+
+
+def bf16_y_excess(y_bits: np.ndarray, ref: np.ndarray, tol: float = 1e-5) -> float:
+    """How far a bf16 output exceeds its bar, as a multiple of the bar (<= 1
+    passes). The bar per element is the fp32 contract plus the output's own
+    rounding: tol * max|ref| over the (row, head) vector (the last dim) plus
+    one bf16 ulp of ref. One ulp alone would be stricter than the fp32
+    contract for outputs near zero, where the summands cancel."""
+    y = O.bf16_bits_to_f64(y_bits).reshape(ref.shape)
+    tile = np.abs(ref).max(axis=-1, keepdims=True)
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) * 65536.0
+    bar = tol * tile + ulp
+    return float(np.max(np.abs(y - ref) / bar))

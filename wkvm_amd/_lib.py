@@ -16,6 +16,10 @@ _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG_DIR, "libwkv7.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "wkv7.h")
 
+# The ABI this binding is written for (WKV7_ABI_VERSION of include/wkv7.h);
+# a library built from other sources is refused at load.
+WKV7_ABI_VERSION = 9
+
 WKV7_OK = 0
 WKV7_ERR_ARG = -1
 WKV7_ERR_SHAPE = -2
@@ -55,10 +59,12 @@ SIGNATURES = {
     "wkv7_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "wkv7_decode_slots": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _f32, _vp]),
+    "wkv7_decode_into": (ctypes.c_int, [
+        _vp, _i64, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _i32, _f32, _vp]),
     "wkv7_prefill_varlen": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
-        _i32, _f32, _vp, _sz, _vp]),
-    "wkv7_prefill_workspace_bytes": (_sz, [_i32, _i32, _i64]),
+        _i32, _f32, _vp]),
     "wkv7_prefill_runs": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
         _i32, _f32, _vp, _vp, _i32, _vp, _i64, _vp, _vp]),
@@ -109,6 +115,13 @@ def load():
                 f"{LIB_PATH} is not built; run `python -m wkvm_amd.build` "
                 "(or __graft_entry__.build()) first -- there is no CPU fallback")
         lib = ctypes.CDLL(LIB_PATH)
+        lib.wkv7_abi_version.restype = ctypes.c_int
+        lib.wkv7_abi_version.argtypes = []
+        found = int(lib.wkv7_abi_version())
+        if found != WKV7_ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} has ABI version {found}, this package needs {WKV7_ABI_VERSION}; "
+                "the library is stale -- rebuild it with `python -m wkvm_amd.build`")
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = res

@@ -14,6 +14,14 @@
 // once and written once), issued with non-temporal hints. Workgroups visit the
 // batch rows in the caller's `row_order` (slot-sorted order keeps the HBM
 // access stream inside a few neighbouring slot regions at a time).
+//
+// The same kernel serves the in-place slot decode (source and destination are
+// one pool and one id list) and the out-of-place form of fla's recurrent op
+// (state read from one tensor, written to another; no source = zero state, no
+// destination = the state is not written). A row whose source or destination
+// id is out of range touches no state and gets y = 0.
+#include <type_traits>
+
 #include "wkv7_common.h"
 #include "wkv7_timemix_head.h"
 
@@ -26,8 +34,9 @@ constexpr int kRowsPerWave = kHead / kDecWaves;  // 16
 // The state update of one (row, head) once the per-key-row vectors (decay,
 // b, k, scale*r, a) of the wave's own rows are staged in LDS and vi is the
 // lane's value: p partials, one barrier, the update with its non-temporal
-// stores, y partials, one barrier. Returns y_i on wave 0 (unspecified on the
-// others).
+// stores (kStore; hp is the wave's first destination row), y partials, one
+// barrier. Returns y_i on wave 0 (unspecified on the others).
+template <bool kStore>
 __device__ __forceinline__ float decode_core(float* hp, float (&h)[kRowsPerWave], int lane,
                                              int wave, const float4* s_dbkr, const float* s_a,
                                              float (*s_p)[kHead], float (*s_y)[kHead], float vi) {
@@ -47,7 +56,7 @@ __device__ __forceinline__ float decode_core(float* hp, float (&h)[kRowsPerWave]
   for (int j = 0; j < kRowsPerWave; ++j) {
     const float4 c = s_dbkr[j0 + j];
     const float hn = fmaf(c.x, h[j], fmaf(c.y, p, c.z * vi));
-    __builtin_nontemporal_store(hn, hp + j * kHead);
+    if (kStore) __builtin_nontemporal_store(hn, hp + j * kHead);
     if (j & 1)
       y1 = fmaf(c.w, hn, y1);
     else
@@ -58,13 +67,46 @@ __device__ __forceinline__ float decode_core(float* hp, float (&h)[kRowsPerWave]
   return (s_y[0][lane] + s_y[1][lane]) + (s_y[2][lane] + s_y[3][lane]);
 }
 
+// State addressing of one decode launch: row b reads src[src_ids[b]] (or
+// src[b] when src_ids is null; zero state when src is null) and writes
+// dst[dst_ids[b]] (dst[b] when dst_ids is null; nothing when dst is null).
+struct DecodeIO {
+  const float* src;
+  const int32_t* src_ids;
+  int64_t src_rows;
+  float* dst;
+  const int32_t* dst_ids;
+  int64_t dst_rows;
+};
+
+// How a launch addresses state; one kernel instantiation per form, so that
+// no branch separates the state loads from their uses (a branch around them
+// makes the compiler wait for every load before the first use).
+enum DecodeForm : int {
+  kInPlace = 0,    // src == dst, one id list (wkv7_decode_slots)
+  kSeparate = 1,   // read src, write dst
+  kZeroIn = 2,     // zero initial state, write dst
+  kNoOut = 3,      // read src, state not written
+  kZeroNoOut = 4,  // zero initial state, state not written
+};
+
 template <bool kF32Out>
+__device__ __forceinline__ void store_y(void* y, int64_t io, float yi) {
+  if (kF32Out)
+    static_cast<float*>(y)[io] = yi;
+  else
+    static_cast<uint16_t*>(y)[io] = f32_to_bf16(yi);
+}
+
+template <bool kF32Out, int kForm>
 __global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
-    float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ row_order, int B, const uint16_t* __restrict__ r,
-    const uint16_t* __restrict__ w, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ a,
-    const uint16_t* __restrict__ b, void* __restrict__ y, float scale) {
+    DecodeIO st, int H, const int32_t* __restrict__ row_order, int B,
+    const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, void* __restrict__ y,
+    float scale) {
+  constexpr bool kLoad = kForm == kInPlace || kForm == kSeparate || kForm == kNoOut;
+  constexpr bool kStore = kForm == kInPlace || kForm == kSeparate || kForm == kZeroIn;
   __shared__ float4 s_dbkr[kHead];            // (decay, b, k, scale*r) per key row j
   __shared__ float s_a[kHead];
   __shared__ float s_p[kDecWaves][kHead];  // per-wave partial p
@@ -79,34 +121,66 @@ __global__ __launch_bounds__(kWave * kDecWaves) void decode_slots_kernel(
     row = row_order[pos];
     if (row < 0 || row >= B) return;  // uniform: the whole block skips
   }
-  const int64_t slot = slot_ids[row];
-  if (slot < 0 || slot >= num_rows) return;
-
-  float* hp = wkv + (slot * H + head) * (kHead * kHead) + (kRowsPerWave * wave) * kHead + lane;
-  float h[kRowsPerWave];
-#pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hp + j * kHead);
-
   const int64_t io = (row * H + head) * kHead + lane;
+  int64_t src_slot = 0, dst_slot = 0;
+  bool ok = true;
+  if (kForm == kInPlace) {
+    src_slot = dst_slot = st.dst_ids[row];
+    ok = dst_slot >= 0 && dst_slot < st.dst_rows;
+  } else {
+    if (kLoad) {
+      src_slot = st.src_ids ? int64_t(st.src_ids[row]) : row;
+      ok = src_slot >= 0 && src_slot < st.src_rows;
+    }
+    if (kStore) {
+      dst_slot = st.dst_ids ? int64_t(st.dst_ids[row]) : row;
+      ok = ok && dst_slot >= 0 && dst_slot < st.dst_rows;
+    }
+  }
+  if (!ok) {  // uniform: a rejected row touches no state and reads out zero
+    if (wave == 0) store_y<kF32Out>(y, io, 0.f);
+    return;
+  }
+
+  // The per-token vectors are loaded before the state rows: load counts
+  // retire in issue order, so waiting for the vectors does not wait for the
+  // state stream, and the staging arithmetic overlaps it. Lanes 16..63 read
+  // the key rows of lanes 0..15 again (same addresses, no extra traffic) so
+  // that no branch separates the loads from the state loads.
   const int j0 = kRowsPerWave * wave;
+  const int64_t jo = (row * H + head) * kHead + j0 + (lane & (kRowsPerWave - 1));
+  const uint16_t wb = w[jo], bb = b[jo], kb = k[jo], rb = r[jo], ab = a[jo], vb = v[io];
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int64_t wave_off = (kRowsPerWave * wave) * kHead + lane;
+  float h[kRowsPerWave];
+  if (kLoad) {
+    const float* hs = (kForm == kInPlace ? st.dst : st.src) +
+                      (src_slot * H + head) * (kHead * kHead) + wave_off;
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hs + j * kHead);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) h[j] = 0.f;
+  }
+  // an empty asm that consumes the vectors here keeps their loads above the
+  // state loads (the compiler would otherwise sink them into the lane < 16
+  // branch); it waits for the vectors only
+  asm volatile("" ::"v"(wb), "v"(bb), "v"(kb), "v"(rb), "v"(ab), "v"(vb));
+
   // Each wave stages the vectors of its own key rows and is their only
   // reader, so a wavefront-scope fence orders the LDS writes before the reads
   // (no workgroup barrier).
   if (lane < kRowsPerWave) {
-    const int64_t jo = io + j0;  // key row j0 + lane
-    s_dbkr[j0 + lane] = make_float4(expf(bf16_to_f32(w[jo])), bf16_to_f32(b[jo]),
-                                    bf16_to_f32(k[jo]), bf16_to_f32(r[jo]) * scale);
-    s_a[j0 + lane] = bf16_to_f32(a[jo]);
+    s_dbkr[j0 + lane] = make_float4(expf(bf16_to_f32(wb)), bf16_to_f32(bb), bf16_to_f32(kb),
+                                    bf16_to_f32(rb) * scale);
+    s_a[j0 + lane] = bf16_to_f32(ab);
   }
-  const float vi = bf16_to_f32(v[io]);
+  const float vi = bf16_to_f32(vb);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const float yi = decode_core(hp, h, lane, wave, s_dbkr, s_a, s_p, s_y, vi);
-  if (wave == 0) {
-    if (kF32Out)
-      static_cast<float*>(y)[io] = yi;
-    else
-      static_cast<uint16_t*>(y)[io] = f32_to_bf16(yi);
-  }
+  float* hd = kStore ? st.dst + (dst_slot * H + head) * (kHead * kHead) + wave_off : nullptr;
+  const float yi = decode_core<kStore>(hd, h, lane, wave, s_dbkr, s_a, s_p, s_y, vi);
+  if (wave == 0) store_y<kF32Out>(y, io, yi);
 }
 
 struct BlockIn {
@@ -122,6 +196,7 @@ struct BlockIn {
 // the work of lanes 0..15), stages its own key rows and its copy of v in LDS,
 // and wave 0 finishes the output. Same arithmetic, in the same order, as
 // wkv7_time_mix_inputs -> wkv7_decode_slots (bf16 y) -> wkv7_time_mix_output.
+template <bool kLerpV>
 __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ row_order, int B, BlockIn in, float eps, float scale,
@@ -143,44 +218,59 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     row = row_order[pos];
     if (row < 0 || row >= B) return;
   }
+  // Lane sub holds channels 4 sub .. 4 sub + 3 of this (row, head). The row's
+  // and the head's element offsets are uniform, so every row input and
+  // parameter is addressed as a uniform base plus the lane's small offset
+  // (scalar base + vector offset; no 64-bit address per lane and input).
+  const int sub = lane & 15;
+  const int64_t ro = (row * H + head) * kHead;  // this row-head's first element
+  const int64_t po = head * kHead;              // this head's first parameter
+  const int o = 4 * sub;
+  const int pc = 4 * sub;
   const int64_t slot = slot_ids[row];
-  if (slot < 0 || slot >= num_rows) return;
+  if (slot < 0 || slot >= num_rows) {  // a rejected row reads out zero
+    if (wave == 0 && lane < 16) {
+      st4(out + ro + o, 0.f, 0.f, 0.f, 0.f);
+      if (v_out) st4(v_out + ro + o, 0.f, 0.f, 0.f, 0.f);
+    }
+    return;
+  }
+
+  // The projection rows are loaded before the state rows (load counts retire
+  // in issue order), so the input arithmetic below waits for them only and
+  // overlaps the state stream.
+  const Bf4 rb = ld4(in.r + ro + o), kb = ld4(in.k + ro + o), vb = ld4(in.v + ro + o),
+            wlb = ld4(in.w_lora + ro + o), alb = ld4(in.a_lora + ro + o);
+  const Bf4 kksb = ld4(in.k_k + po + pc), kab = ld4(in.k_a + po + pc);
+  Bf4 vlb = {}, vfb = {};
+  if (kLerpV) {
+    vlb = ld4(in.v_lora + ro + o);
+    vfb = ld4(in.v_first + ro + o);
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
   float* hp = wkv + (slot * H + head) * (kHead * kHead) + (kRowsPerWave * wave) * kHead + lane;
   float h[kRowsPerWave];
 #pragma unroll
   for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hp + j * kHead);
 
-  // channels 4 sub .. 4 sub + 3 of this (row, head)
-  const int sub = lane & 15;
-  const int64_t o = (row * H + head) * kHead + 4 * sub;
-  const int pc = int(head * kHead + 4 * sub);
   float rr[4], k[4], v[4], wl[4], al[4], kks[4], ka[4], vl[4] = {}, vf[4] = {};
-  {
-    const Bf4 rb = ld4(in.r + o), kb = ld4(in.k + o), vb = ld4(in.v + o),
-              wlb = ld4(in.w_lora + o), alb = ld4(in.a_lora + o);
-    const Bf4 kksb = ld4(in.k_k + pc), kab = ld4(in.k_a + pc);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      rr[e] = el(rb, e);
-      k[e] = el(kb, e);
-      v[e] = el(vb, e);
-      wl[e] = el(wlb, e);
-      al[e] = el(alb, e);
-      kks[e] = el(kksb, e);
-      ka[e] = el(kab, e);
-    }
-    if (in.v_lora) {
-      const Bf4 vlb = ld4(in.v_lora + o), vfb = ld4(in.v_first + o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vl[e] = el(vlb, e);
-        vf[e] = el(vfb, e);
-      }
+  for (int e = 0; e < 4; ++e) {
+    rr[e] = el(rb, e);
+    k[e] = el(kb, e);
+    v[e] = el(vb, e);
+    wl[e] = el(wlb, e);
+    al[e] = el(alb, e);
+    kks[e] = el(kksb, e);
+    ka[e] = el(kab, e);
+    if (kLerpV) {
+      vl[e] = el(vlb, e);
+      vf[e] = el(vfb, e);
     }
   }
   float wv[4], kv[4], vv[4], av[4], bv[4];
-  head_inputs(k, v, wl, al, kks, ka, in.v_lora != nullptr, vl, vf, wv, kv, vv, av, bv);
+  head_inputs(k, v, wl, al, kks, ka, kLerpV, vl, vf, wv, kv, vv, av, bv);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     wv[e] = round_bf16(wv[e]);
@@ -203,7 +293,7 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const float vi = s_v[wave][lane];
-  const float yi = decode_core(hp, h, lane, wave, s_dbkr, s_a, s_p, s_y, vi);
+  const float yi = decode_core<true>(hp, h, lane, wave, s_dbkr, s_a, s_p, s_y, vi);
   if (wave == 0) {
     // y goes to the output stage rounded to bf16, as the unfused path stores
     // it; r, k and v come back from LDS (every wave's rows are visible after
@@ -211,8 +301,8 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     s_yo[lane] = round_bf16(yi);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float y4[4], r4[4], k4[4], v4[4], g[4], rk[4], lw[4], lb[4], ov[4];
-    const Bf4 gb = ld4(in.g + o), rkb = ld4(in.r_k + pc), lwb = ld4(in.ln_w + pc),
-              lbb = ld4(in.ln_b + pc);
+    const Bf4 gb = ld4(in.g + ro + o), rkb = ld4(in.r_k + po + pc), lwb = ld4(in.ln_w + po + pc),
+              lbb = ld4(in.ln_b + po + pc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = 4 * sub + e;
@@ -227,8 +317,8 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     }
     head_output(y4, r4, k4, v4, g, rk, lw, lb, eps, ov);
     if (lane < 16) {
-      st4(out + o, ov[0], ov[1], ov[2], ov[3]);
-      if (v_out) st4(v_out + o, v4[0], v4[1], v4[2], v4[3]);
+      st4(out + ro + o, ov[0], ov[1], ov[2], ov[3]);
+      if (v_out) st4(v_out + ro + o, v4[0], v4[1], v4[2], v4[3]);
     }
   }
 }
@@ -238,26 +328,81 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
 
 using namespace wkv7;
 
+static int launch_decode(const DecodeIO& st, int32_t H, const int32_t* row_order, int32_t B,
+                         const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                         const uint16_t* v, const uint16_t* a, const uint16_t* b, void* y,
+                         int32_t y_dtype, float scale, void* stream) {
+  if (B < 0 || H < 1) return WKV7_ERR_ARG;
+  if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
+  if ((st.src && st.src_rows < 1) || (st.dst && st.dst_rows < 1)) return WKV7_ERR_ARG;
+  if (B == 0) return WKV7_OK;
+  if (!r || !w || !k || !v || !a || !b || !y) return WKV7_ERR_ARG;
+  const int64_t blocks = int64_t(B) * H;
+  if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
+  int form = kSeparate;
+  if (st.src && st.src == st.dst && st.src_ids && st.src_ids == st.dst_ids &&
+      st.src_rows == st.dst_rows)
+    form = kInPlace;
+  else if (!st.src)
+    form = st.dst ? kZeroIn : kZeroNoOut;
+  else if (!st.dst)
+    form = kNoOut;
+  hipStream_t s = as_stream(stream);
+  const unsigned grid = unsigned(blocks), threads = kWave * kDecWaves;
+  auto launch = [&](auto f32) {
+    constexpr bool F = decltype(f32)::value;
+    switch (form) {
+      case kInPlace:
+        decode_slots_kernel<F, kInPlace><<<grid, threads, 0, s>>>(st, H, row_order, B, r, w, k,
+                                                                  v, a, b, y, scale);
+        break;
+      case kSeparate:
+        decode_slots_kernel<F, kSeparate><<<grid, threads, 0, s>>>(st, H, row_order, B, r, w, k,
+                                                                   v, a, b, y, scale);
+        break;
+      case kZeroIn:
+        decode_slots_kernel<F, kZeroIn><<<grid, threads, 0, s>>>(st, H, row_order, B, r, w, k,
+                                                                 v, a, b, y, scale);
+        break;
+      case kNoOut:
+        decode_slots_kernel<F, kNoOut><<<grid, threads, 0, s>>>(st, H, row_order, B, r, w, k, v,
+                                                                a, b, y, scale);
+        break;
+      default:
+        decode_slots_kernel<F, kZeroNoOut><<<grid, threads, 0, s>>>(st, H, row_order, B, r, w, k,
+                                                                    v, a, b, y, scale);
+    }
+  };
+  if (y_dtype == WKV7_Y_F32)
+    launch(std::true_type{});
+  else
+    launch(std::false_type{});
+  return launch_status();
+}
+
 extern "C" int wkv7_decode_slots(float* wkv_layer, int64_t num_rows, int32_t H,
                                  const int32_t* slot_ids, const int32_t* row_order, int32_t B,
                                  const uint16_t* r, const uint16_t* w, const uint16_t* k,
                                  const uint16_t* v, const uint16_t* a, const uint16_t* b, void* y,
                                  int32_t y_dtype, float scale, void* stream) {
-  if (B < 0 || H < 1 || num_rows < 1) return WKV7_ERR_ARG;
-  if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
-  if (B == 0) return WKV7_OK;
-  if (!wkv_layer || !slot_ids || !r || !w || !k || !v || !a || !b || !y) return WKV7_ERR_ARG;
-  const int64_t blocks = int64_t(B) * H;
-  if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
-  hipStream_t s = as_stream(stream);
-  const unsigned threads = kWave * kDecWaves;
-  if (y_dtype == WKV7_Y_F32)
-    decode_slots_kernel<true><<<unsigned(blocks), threads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, row_order, B, r, w, k, v, a, b, y, scale);
-  else
-    decode_slots_kernel<false><<<unsigned(blocks), threads, 0, s>>>(
-        wkv_layer, num_rows, H, slot_ids, row_order, B, r, w, k, v, a, b, y, scale);
-  return launch_status();
+  if (num_rows < 1) return WKV7_ERR_ARG;
+  if (B > 0 && (!wkv_layer || !slot_ids)) return WKV7_ERR_ARG;
+  const DecodeIO st{wkv_layer, slot_ids, num_rows, wkv_layer, slot_ids, num_rows};
+  return launch_decode(st, H, row_order, B, r, w, k, v, a, b, y, y_dtype, scale, stream);
+}
+
+extern "C" int wkv7_decode_into(const float* state_in, int64_t in_rows, const int32_t* in_ids,
+                                float* state_out, int64_t out_rows, const int32_t* out_ids,
+                                int32_t H, const int32_t* row_order, int32_t B,
+                                const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                                const uint16_t* v, const uint16_t* a, const uint16_t* b, void* y,
+                                int32_t y_dtype, float scale, void* stream) {
+  if ((!state_in && in_ids) || (!state_out && out_ids)) return WKV7_ERR_ARG;
+  // without ids, row b addresses state row b: the tensor needs B rows
+  if ((state_in && !in_ids && in_rows < B) || (state_out && !out_ids && out_rows < B))
+    return WKV7_ERR_SHAPE;
+  const DecodeIO st{state_in, in_ids, in_rows, state_out, out_ids, out_rows};
+  return launch_decode(st, H, row_order, B, r, w, k, v, a, b, y, y_dtype, scale, stream);
 }
 
 extern "C" int wkv7_decode_block(float* wkv_layer, int64_t num_rows, int32_t H,
@@ -284,7 +429,11 @@ extern "C" int wkv7_decode_block(float* wkv_layer, int64_t num_rows, int32_t H,
   const int64_t blocks = int64_t(B) * H;
   if (blocks > int64_t(0x7fffffff)) return WKV7_ERR_ARG;
   const BlockIn in{r, k, v, w_lora, a_lora, v_lora, v_first, g, k_k, k_a, r_k, ln_w, ln_b};
-  decode_block_kernel<<<unsigned(blocks), kWave * kDecWaves, 0, as_stream(stream)>>>(
-      wkv_layer, num_rows, H, slot_ids, row_order, B, in, eps, scale, out, v_out);
+  if (v_lora)
+    decode_block_kernel<true><<<unsigned(blocks), kWave * kDecWaves, 0, as_stream(stream)>>>(
+        wkv_layer, num_rows, H, slot_ids, row_order, B, in, eps, scale, out, v_out);
+  else
+    decode_block_kernel<false><<<unsigned(blocks), kWave * kDecWaves, 0, as_stream(stream)>>>(
+        wkv_layer, num_rows, H, slot_ids, row_order, B, in, eps, scale, out, v_out);
   return launch_status();
 }

@@ -667,13 +667,6 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 
 using namespace wkv7;
 
-extern "C" size_t wkv7_prefill_workspace_bytes(int32_t H, int32_t nseq, int64_t total_tokens) {
-  (void)H;
-  (void)nseq;
-  (void)total_tokens;
-  return 0;
-}
-
 namespace {
 int prefill_launch(float* wkv_layer, int64_t num_rows, int32_t H, const int32_t* slot_ids,
                    const int32_t* cu_seqlens, const int32_t* seq_order, int32_t nseq,
@@ -717,16 +710,13 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
                                    const uint16_t* r,
                                    const uint16_t* w, const uint16_t* k, const uint16_t* v,
                                    const uint16_t* a, const uint16_t* b, void* y, int32_t y_dtype,
-                                   int32_t zero_init, float scale, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+                                   int32_t zero_init, float scale, void* stream) {
   if (nseq < 0 || H < 1 || num_rows < 1 || total_tokens < 0) return WKV7_ERR_ARG;
   if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
   if (nseq == 0) return WKV7_OK;
   if (!wkv_layer || !slot_ids || !cu_seqlens) return WKV7_ERR_ARG;
   if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
   if (!inputs_aligned(r, w, k, v, a, b)) return WKV7_ERR_SHAPE;
-  if (workspace_bytes < wkv7_prefill_workspace_bytes(H, nseq, total_tokens)) return WKV7_ERR_WORKSPACE;
-  (void)workspace;
   const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr};
   return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
                         total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,

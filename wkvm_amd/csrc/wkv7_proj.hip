@@ -83,15 +83,16 @@ __device__ __forceinline__ uint32_t lds_addr(const uint4* p) {
 }
 
 // Direct load: 16 bytes per lane from global memory into LDS, lane l's bytes
-// at lds_base + 16 l (lds_base is wave-uniform, passed in M0; one wait state
-// separates the M0 write from its use). Issued as inline assembly so that the
+// at lds_base + 16 l (lds_base is wave-uniform and bound to M0 as an input
+// operand, so the compiler writes M0 itself and knows its value; one wait
+// state separates that write from its use). Issued as inline assembly so that the
 // compiler's wait insertion neither sees these LDS writes (it would wait for
 // every pending direct load before any LDS read) nor counts them: all waits
 // for them are the explicit ones of stage_barrier below.
 __device__ __forceinline__ void load_lds16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
-               : "s"(lds_base), "v"(src)
+               : "{m0}"(lds_base), "v"(src)
                : "memory");
 }
 

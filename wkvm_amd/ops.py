@@ -176,6 +176,76 @@ def wkv7_decode_slots(wkv_layer: torch.Tensor, slot_ids, r, w, k, v, a, b, *,
     return y
 
 
+def _state_tensor(t: torch.Tensor | None, H: int, device: torch.device, what: str) -> int:
+    """Rows of an optional ``[rows, H, 64, 64]`` fp32 state tensor (0 for None)."""
+    if t is None:
+        return 0
+    rows, heads = _check_pool(t)
+    if heads != H:
+        raise ValueError(f"{what} has {heads} heads, the inputs {H}")
+    if t.device != device:
+        raise ValueError(f"{what} on {t.device}, inputs on {device}")
+    return rows
+
+
+def wkv7_decode_into(state_in: torch.Tensor | None, state_out: torch.Tensor | None,
+                     r, w, k, v, a, b, *, in_ids=None, out_ids=None, scale: float = 1.0,
+                     out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                     row_order: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token per row with the state read from ``state_in`` and
+    written to ``state_out`` (each ``[rows, H, 64, 64]`` fp32, or None: a zero
+    initial state / no state written). Row ``b`` reads ``state_in[in_ids[b]]``
+    and writes ``state_out[out_ids[b]]``; ``None`` ids mean row ``b``. This is
+    fla's recurrent op at seq_len 1 (initial_state -> final_state) without a
+    copy of the state. Returns ``y [B, H, 64]``."""
+    _require_cuda(r, "decode.r")
+    if r.dim() != 3:
+        raise ValueError(f"decode inputs must be [B, H, 64], got {tuple(r.shape)}")
+    B, H = int(r.shape[0]), int(r.shape[1])
+    dev = r.device
+    xs = _check_vectors((r, w, k, v, a, b), (B, H, HEAD_SIZE), dev, "decode")
+    in_rows = _state_tensor(state_in, H, dev, "state_in")
+    out_rows = _state_tensor(state_out, H, dev, "state_out")
+    if in_ids is not None and state_in is None:
+        raise ValueError("in_ids without state_in")
+    if out_ids is not None and state_out is None:
+        raise ValueError("out_ids without state_out")
+    for t, ids, n in ((state_in, in_ids, "state_in"), (state_out, out_ids, "state_out")):
+        if t is not None and ids is None and t.shape[0] < B:
+            raise ValueError(f"{n} has {t.shape[0]} rows for {B} batch rows")
+    if state_in is not None and state_out is not None and _overlaps(state_in, state_out):
+        # in place row by row, or disjoint row sets; anything else would let a
+        # row overwrite a state another row still has to read
+        if state_in.data_ptr() != state_out.data_ptr():
+            raise ValueError("state_in and state_out overlap at different offsets")
+        if not all(isinstance(x, _IDS) or x is None for x in (in_ids, out_ids)):
+            raise ValueError("overlapping state tensors need host ids (checked here)")
+        src = list(range(B)) if in_ids is None else [int(i) for i in in_ids]
+        dst = list(range(B)) if out_ids is None else [int(i) for i in out_ids]
+        if src != dst and set(src) & set(dst):
+            raise ValueError("a row writes a state row that another row reads")
+    d_in = None if in_ids is None else device_ids(in_ids, in_rows, dev, "in_ids", distinct=False)
+    d_out = None if out_ids is None else device_ids(out_ids, out_rows, dev, "out_ids",
+                                                    distinct=True)
+    for ids in (d_in, d_out):
+        if ids is not None and int(ids.shape[0]) != B:
+            raise ValueError(f"{int(ids.shape[0])} ids for {B} batch rows")
+    if row_order is not None and not (isinstance(row_order, torch.Tensor) and row_order.is_cuda
+                                      and row_order.dtype == torch.int32
+                                      and tuple(row_order.shape) == (B,)):
+        raise ValueError("row_order must be a device int32 tensor of B entries")
+    code = _y_code(out.dtype if out is not None else out_dtype)
+    y = _out(out, (B, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
+    if B == 0:
+        return y
+    rc = _lib.load().wkv7_decode_into(_ptr(state_in), in_rows, _ptr(d_in), _ptr(state_out),
+                                      out_rows, _ptr(d_out), H, _ptr(row_order), B,
+                                      *[x.data_ptr() for x in xs], y.data_ptr(), code,
+                                      float(scale), _stream_ptr(dev))
+    _lib.check(rc, "wkv7_decode_into")
+    return y
+
+
 def _host_cu(cu, T: int) -> list[int]:
     if isinstance(cu, torch.Tensor):
         cu = cu.tolist()
@@ -190,10 +260,6 @@ def _host_cu(cu, T: int) -> list[int]:
     return lst
 
 
-def prefill_workspace_bytes(H: int, nseq: int, total_tokens: int) -> int:
-    return int(_lib.load().wkv7_prefill_workspace_bytes(int(H), int(nseq), int(total_tokens)))
-
-
 def longest_first(cu: Sequence[int]) -> list[int]:
     """Sequence order for a ragged prefill launch: longest first (ties in
     index order), which packs the per-(sequence, head) workgroups onto the
@@ -206,7 +272,6 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
                         zero_init: bool = False, scale: float = 1.0,
                         out: torch.Tensor | None = None,
                         out_dtype: torch.dtype = torch.bfloat16,
-                        workspace: torch.Tensor | None = None,
                         seq_order: torch.Tensor | None = None) -> torch.Tensor:
     """Ragged prefill: sequence ``s`` runs tokens ``cu_seqlens[s]:cu_seqlens[s+1]``
     of the ``[T, H, 64]`` bf16 inputs from slot ``slot_ids[s]`` (or zero state
@@ -242,20 +307,10 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
     y = _out(out, (T, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
     if nseq == 0:
         return y
-    lib = _lib.load()
-    need = int(lib.wkv7_prefill_workspace_bytes(H, nseq, T))
-    if need > 0:
-        if workspace is None:
-            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-        elif workspace.numel() * workspace.element_size() < need:
-            raise ValueError(f"workspace needs {need} bytes")
-    ws_ptr = workspace.data_ptr() if (workspace is not None and need > 0) else None
-    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
-    rc = lib.wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(), cu.data_ptr(),
-                                 _ptr(seq_order), nseq, T, *[x.data_ptr() for x in xs],
-                                 y.data_ptr(), code,
-                                 int(bool(zero_init)), float(scale), ws_ptr, ws_bytes,
-                                 _stream_ptr(dev))
+    rc = _lib.load().wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(),
+                                         cu.data_ptr(), _ptr(seq_order), nseq, T,
+                                         *[x.data_ptr() for x in xs], y.data_ptr(), code,
+                                         int(bool(zero_init)), float(scale), _stream_ptr(dev))
     _lib.check(rc, "wkv7_prefill_varlen")
     return y
 
@@ -834,44 +889,62 @@ def auto_segments(H: int, lens: Sequence[int], device: torch.device) -> int:
     return max(1, min(4, (cus // busy + 1) // 2))
 
 
+def _fla_state(initial_state, nseq: int, H: int, dev: torch.device) -> torch.Tensor | None:
+    if initial_state is None:
+        return None
+    if tuple(initial_state.shape) != (nseq, H, HEAD_SIZE, HEAD_SIZE):
+        raise ValueError(f"initial_state must be {(nseq, H, HEAD_SIZE, HEAD_SIZE)}, "
+                         f"got {tuple(initial_state.shape)}")
+    return initial_state.to(device=dev, dtype=torch.float32).contiguous()
+
+
 def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens, head_first):
+    """fla's wkv-op contract: ``[B, T, H, 64]`` inputs (or ``[1, T_total, H,
+    64]`` packed by ``cu_seqlens``), ``initial_state`` read, a new
+    ``final_state`` returned. One token per sequence runs the decode kernel
+    out of place (initial_state -> final_state, no copy); longer sequences run
+    the chunked scan on a copy of initial_state."""
     if head_first:
         r, w, k, v, a, b = (x.transpose(1, 2) for x in (r, w, k, v, a, b))
     _require_cuda(r, "r")
     if r.dim() != 4:
         raise ValueError("inputs must be [B, T, H, K]")
-    B, T, H, K = r.shape
+    B, T, H, K = (int(d) for d in r.shape)
     if K != HEAD_SIZE:
         raise ValueError(f"head size must be {HEAD_SIZE}, got {K}")
     if r.dtype != torch.bfloat16:
         raise ValueError("the gfx950 WKV7 kernels take bfloat16 inputs")
     if cu_seqlens is None:
         nseq = B
-        cu = [i * T for i in range(B + 1)]
+        host_cu = [i * T for i in range(B + 1)]
         flat = [x.reshape(B * T, H, K) for x in (r, w, k, v, a, b)]
     else:
         if B != 1:
             raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
-        cu = cu_seqlens
-        nseq = (len(cu) if not isinstance(cu, torch.Tensor) else int(cu.numel())) - 1
+        # fla passes a device LongTensor; the offsets are validated on the host
+        host_cu = _host_cu(cu_seqlens, T)
+        nseq = len(host_cu) - 1
         flat = [x[0] for x in (r, w, k, v, a, b)]
     dev = r.device
-    if initial_state is not None:
-        if tuple(initial_state.shape) != (nseq, H, K, K):
-            raise ValueError(f"initial_state must be {(nseq, H, K, K)}")
-        pool = initial_state.to(device=dev, dtype=torch.float32).clone().contiguous()
-    else:
+    state = _fla_state(initial_state, nseq, H, dev)
+    lens = [host_cu[i + 1] - host_cu[i] for i in range(nseq)]
+    if nseq and all(n == 1 for n in lens):  # decode: one token per sequence
+        final = (torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
+                 if output_final_state else None)
+        y = wkv7_decode_into(state, final, *flat, scale=scale, out_dtype=r.dtype)
+        o = y.reshape(B, T, H, K)
+        return (o.transpose(1, 2) if head_first else o), final
+    if state is None:
         pool = torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
-    host_cu = cu.tolist() if isinstance(cu, torch.Tensor) else [int(c) for c in cu]
-    G = auto_segments(H, [host_cu[i + 1] - host_cu[i] for i in range(nseq)], dev)
+    else:
+        pool = state.clone() if state is initial_state else state
+    G = auto_segments(H, lens, dev)
     if G > 1:  # few long sequences: run their segments side by side
         y = wkv7_prefill_segments(pool, list(range(nseq)), host_cu, *flat, segments=G,
-                                  zero_init=initial_state is None, scale=scale,
-                                  out_dtype=r.dtype)
+                                  zero_init=state is None, scale=scale, out_dtype=r.dtype)
     else:
-        ids = torch.arange(nseq, dtype=torch.int32, device=dev)
-        y = wkv7_prefill_varlen(pool, ids, cu, *flat, zero_init=initial_state is None,
-                                scale=scale, out_dtype=r.dtype)
+        y = wkv7_prefill_varlen(pool, list(range(nseq)), host_cu, *flat,
+                                zero_init=state is None, scale=scale, out_dtype=r.dtype)
     o = y.reshape(B, T, H, K)
     if head_first:
         o = o.transpose(1, 2)

@@ -152,7 +152,7 @@ class RWKV7StateBank:
 
     def prefill_wkv(self, layer: int, slot_batch, cu_seqlens, r, w, k, v, a, b, *,
                     zero_init: bool = False, scale: float = 1.0, out=None,
-                    out_dtype: torch.dtype = torch.bfloat16, workspace=None,
+                    out_dtype: torch.dtype = torch.bfloat16,
                     seq_order=None) -> torch.Tensor:
         """Ragged prefill for ``layer``: sequence s of the packed ``[T, H, 64]``
         inputs continues from (or, with ``zero_init``, replaces) its slot state.
@@ -160,8 +160,7 @@ class RWKV7StateBank:
         ids = slot_batch if isinstance(slot_batch, torch.Tensor) else ops.ids_list(slot_batch, "wkv")
         return ops.wkv7_prefill_varlen(self.wkv[layer], ids, cu_seqlens, r, w, k, v, a, b,
                                        zero_init=zero_init, scale=scale, out=out,
-                                       out_dtype=out_dtype, workspace=workspace,
-                                       seq_order=seq_order)
+                                       out_dtype=out_dtype, seq_order=seq_order)
 
     def state_bytes(self) -> int:
         return (self.wkv.numel() * self.wkv.element_size()
