@@ -448,6 +448,31 @@ int wkv7_proj_grouped(int64_t m, const wkv7_proj_group *groups, int32_t ngroups,
  * one bf16 ulp of the exact product; each is deterministic. */
 size_t wkv7_proj_workspace_bytes(int64_t m, const wkv7_proj_group *groups, int32_t ngroups);
 
+/*
+ * wkv7_proj_grouped with no workspace argument and no allocation of any kind:
+ * when the launch splits k, the fp32 partials go to a library-owned static
+ * device array of WKV7_PROJ_STATIC_SCRATCH_BYTES on each GPU (held until the
+ * process ends; its address is looked up once per device, on the first call
+ * made with that device current). Same products, same split decision and
+ * bit-identical results as wkv7_proj_grouped given the workspace
+ * wkv7_proj_workspace_bytes asks for.
+ *
+ * No counterpart in the reference. It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops and
+ * harnesses that forbid hipMalloc.
+ *
+ * Limits: a split needing more than WKV7_PROJ_STATIC_SCRATCH_BYTES of
+ * partials returns WKV7_ERR_WORKSPACE (nothing is enqueued); on a 256-unit
+ * MI355X the split plan needs at most 4 MiB. Every call on one GPU shares
+ * that GPU's array and leaves its partials there: calls that overlap on one
+ * GPU (on different streams, or from several host threads) race. Each split
+ * launch writes every partial it later sums, so nothing needs clearing.
+ */
+#define WKV7_PROJ_STATIC_SCRATCH_BYTES (8u * 1024u * 1024u)
+
+int wkv7_proj_grouped_noalloc(int64_t m, const wkv7_proj_group *groups, int32_t ngroups,
+                              void *stream);
+
 #ifdef __cplusplus
 }
 #endif

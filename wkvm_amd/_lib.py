@@ -34,6 +34,7 @@ WKV7_RUN_STATE_ALT = 16
 WKV7_TO_HOST = 0
 WKV7_FROM_HOST = 1
 WKV7_PROJ_MAX_GROUPS = 8
+WKV7_PROJ_STATIC_SCRATCH_BYTES = 8 * 1024 * 1024
 WKV7_ACT_NONE = 0
 WKV7_ACT_TANH = 1
 WKV7_ACT_SIGMOID = 2
@@ -85,6 +86,7 @@ SIGNATURES = {
         _i64, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
     "wkv7_proj_grouped": (ctypes.c_int, [_i64, ctypes.POINTER(ProjGroup), _i32, _vp, _sz, _vp]),
     "wkv7_proj_workspace_bytes": (_sz, [_i64, ctypes.POINTER(ProjGroup), _i32]),
+    "wkv7_proj_grouped_noalloc": (ctypes.c_int, [_i64, ctypes.POINTER(ProjGroup), _i32, _vp]),
     "wkv7_decode_block": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _i32] + [_vp] * 13 + [_f32, _f32, _vp, _vp, _vp]),
 }

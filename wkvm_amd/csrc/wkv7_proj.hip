@@ -26,6 +26,7 @@
 // workgroups per tile (fp32 partials in a caller-provided workspace, summed
 // in part order by proj_reduce_kernel).
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "wkv7_common.h"
@@ -463,6 +464,42 @@ int device_cus(int* cus) {
 }  // namespace
 }  // namespace wkv7
 
+namespace wkv7 {
+namespace {
+
+// Split-k partials of wkv7_proj_grouped_noalloc: a library-owned device array,
+// one per GPU (each device holds its own copy until the process ends). Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in symbol); it passes the device address hipGetSymbolAddress returns
+// for the current device, looked up once per device and kept below.
+static __device__ __align__(256) float scratch[WKV7_PROJ_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call made
+// with that device current).
+int scratch_address(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return WKV7_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return WKV7_ERR_WORKSPACE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
+  return WKV7_OK;
+}
+
+}  // namespace
+}  // namespace wkv7
+
 extern "C" size_t wkv7_proj_workspace_bytes(int64_t m, const wkv7_proj_group* groups,
                                             int32_t ngroups) {
   if (validate(m, groups, ngroups) != WKV7_OK || m == 0) return 0;
@@ -484,6 +521,27 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
   if (p.parts > 1 && (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)))
     p.parts = 1;
   float* ws = static_cast<float*>(workspace);
+  hipStream_t s = as_stream(stream);
+  if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
+}
+
+extern "C" int wkv7_proj_grouped_noalloc(int64_t m, const wkv7_proj_group* groups,
+                                         int32_t ngroups, void* stream) {
+  const int rc = validate(m, groups, ngroups);
+  if (rc != WKV7_OK) return rc;
+  if (m == 0) return WKV7_OK;
+  int cus = 0;
+  const int drc = device_cus(&cus);
+  if (drc != WKV7_OK) return drc;
+  const Plan p = make_plan(m, groups, ngroups, cus);
+  float* ws = nullptr;
+  if (p.parts > 1) {
+    // the split needs more partials than the static buffer holds
+    if (p.ws_bytes > WKV7_PROJ_STATIC_SCRATCH_BYTES) return WKV7_ERR_WORKSPACE;
+    const int src = scratch_address(&ws);
+    if (src != WKV7_OK) return src;
+  }
   hipStream_t s = as_stream(stream);
   if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
   return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
