@@ -58,7 +58,7 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--only", choices=("fla_decode", "fork_decode_7b", "mixed_ragged",
-                                       "decode_graph", "state_store", "time_mix"),
+                                       "decode_graph", "state_store", "time_mix", "proj"),
                     help="run just this extra section and print its result as JSON (for "
                          "rocprofv3 runs; not the benchmark line)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -232,6 +232,103 @@ def bench_fla_decode(torch, dev, args):
     log(f"fla decode cfg1: {ms:.3f} ms/step ({res['slot_steps_per_s']:.0f} slot-steps/s), "
         f"{res['hbm_gbps']:.0f} GB/s = {res['hbm_frac']:.3f} of peak")
     del states, sets
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_proj(torch, dev, args):
+    """The 1.5B time-mix block's projection launches at decode size (256 rows)
+    on wkv7_proj_grouped, timed on their own: stage 1 (r, k, v and the four
+    LoRA down-projections, 7 products, 27.3 MB of weights), stage 2 (the four
+    LoRA up-projections) and o_proj. Each sweep runs one launch per layer over
+    24 layers' distinct weights and inputs (0.9 GB, beyond the 256 MB
+    Infinity Cache); algorithmic bytes = weights + the distinct x rows + the
+    outputs."""
+    import ctypes
+
+    from wkvm_amd import _lib
+    from wkvm_amd.layout import RWKV7StateLayout
+    from wkvm_amd.timemix import RWKV7TimeMix
+
+    L, M = 24, 256
+    lay = RWKV7StateLayout.for_shape("1.5B")
+    D = lay.hidden_size
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    gdev = torch.Generator(device=dev)
+    gdev.manual_seed(args.seed + 31)
+
+    def rows(n):
+        return (torch.randn((M, n), generator=gdev, device=dev)).to(torch.bfloat16)
+
+    keep, launches = [], {"stage1": [], "stage2": [], "o_proj": []}
+    nbytes = {"stage1": 0, "stage2": 0, "o_proj": 0}
+
+    def group_array(prods):
+        arr = (_lib.ProjGroup * len(prods))()
+        total = 0
+        xs_seen = set()
+        for i, (x, w, bias, act) in enumerate(prods):
+            y = torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=dev)
+            keep.append(y)
+            arr[i] = _lib.ProjGroup(x.data_ptr(), w.data_ptr(),
+                                    None if bias is None else bias.data_ptr(), y.data_ptr(),
+                                    x.stride(0), w.stride(0), y.stride(0), w.shape[0],
+                                    w.shape[1], _lib.WKV7_ACT_NONE if act is None else act, 0)
+            total += w.numel() * 2 + y.numel() * 2 + (0 if bias is None else bias.numel() * 2)
+            if x.data_ptr() not in xs_seen:
+                xs_seen.add(x.data_ptr())
+                total += x.numel() * 2
+        return arr, total
+
+    for layer in range(L):
+        W = RWKV7TimeMix.random(lay, 1, dev, seed=args.seed + layer).w
+        keep.append(W)
+        xr, xw, xk, xv, xa, xg = (rows(D) for _ in range(6))
+        hw, ha, hg, hv = rows(W["w1"].shape[0]), rows(W["a1"].shape[0]), rows(W["g1"].shape[0]), \
+            rows(W["v1"].shape[0])
+        o_in = rows(D)
+        keep.extend([xr, xw, xk, xv, xa, xg, hw, ha, hg, hv, o_in])
+        stages = {
+            "stage1": [(xr, W["r"], None, None), (xk, W["k"], None, None), (xv, W["v"], None, None),
+                       (xw, W["w1"], None, _lib.WKV7_ACT_TANH), (xa, W["a1"], None, None),
+                       (xg, W["g1"], None, _lib.WKV7_ACT_SIGMOID), (xv, W["v1"], None, None)],
+            "stage2": [(hw, W["w2"], W["w0"], None), (ha, W["a2"], W["a0"], None),
+                       (hg, W["g2"], None, None), (hv, W["v2"], W["v0"], None)],
+            "o_proj": [(o_in, W["o"], None, None)],
+        }
+        for name, prods in stages.items():
+            arr, total = group_array(prods)
+            ws_bytes = int(lib.wkv7_proj_workspace_bytes(M, arr, len(prods)))
+            ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+            keep.extend([arr, ws])
+            launches[name].append((arr, len(prods), ws.data_ptr() if ws_bytes else None, ws_bytes))
+            nbytes[name] = total
+
+    def sweep(name):
+        for arr, n, ws, wsb in launches[name]:
+            rc = lib.wkv7_proj_grouped(M, arr, n, ws, wsb, stream)
+            if rc:
+                _lib.check(rc, "wkv7_proj_grouped")
+
+    res = {}
+    for name in launches:
+        for _ in range(2):
+            sweep(name)
+        torch.cuda.synchronize()
+        reps = max(3, args.steps // 10)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            sweep(name)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+        res[name] = {"us_per_launch": us, "algorithmic_bytes": nbytes[name],
+                     "hbm_frac": nbytes[name] / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS}
+        log(f"proj {name} at {M} rows: {us:.2f} us per launch, {nbytes[name] / 1e6:.1f} MB "
+            f"-> {res[name]['hbm_frac']:.3f} of HBM peak")
+    del keep, launches
     torch.cuda.empty_cache()
     return res
 
@@ -893,6 +990,7 @@ def main() -> int:
         return 0
     if args.only:
         fn = {"fla_decode": lambda: bench_fla_decode(torch, dev, args),
+              "proj": lambda: bench_proj(torch, dev, args),
               "fork_decode_7b": lambda: bench_fork_decode_7b(torch, dev, args, launcher),
               "mixed_ragged": lambda: bench_mixed(torch, dev, args, launcher),
               "decode_graph": lambda: bench_decode_graph(torch, dev, args),
@@ -910,6 +1008,7 @@ def main() -> int:
         extra["decode_graph"] = bench_decode_graph(torch, dev, args)
         extra["state_store"] = bench_store(torch, dev, args)
         extra["time_mix"] = bench_time_mix(torch, dev, args)
+        extra["proj"] = bench_proj(torch, dev, args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     line = {
         "metric": "WKV7 decode slot-steps/s + achieved HBM GB/s; chunked-prefill tokens/s",
