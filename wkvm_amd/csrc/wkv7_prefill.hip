@@ -37,7 +37,8 @@
 // accumulator holds D[4lg..4lg+3][li]. Contractions over 16 tokens put
 // k = 4lg..4lg+3 in elements 0..3 of both operands and zeros in 4..7; with
 // that labelling a 16x16 accumulator is already the B operand of the next
-// 16-token product, straight from registers. Contractions over the 64 key
+// 16-token product, straight from registers, and an LDS transpose read of
+// token rows 4lg..4lg+3 is the A operand B~^T / K~^T or the B operand v. Contractions over the 64 key
 // rows take the k labels of a 32-row block in the order the state tiles hold
 // them (key_pos below), so the state is a B operand straight from registers
 // as well.
@@ -56,19 +57,20 @@ constexpr int kRing = 4;
 constexpr int kOpWaves = 4;                      // operand wavefronts
 constexpr int kChan = kHead / (4 * kOpWaves);  // key channels per operand lane
 constexpr int kThreads = kWave * (8 + kOpWaves);  // 4 state + operand + 4 score waves
-// LDS layouts. The [row][64] operand arrays have unpadded 128 B rows whose
-// 16 B chunks are XOR-swizzled by the row (chunk c of row r sits at c ^ (r & 7)):
-// the MFMA operand loads (16 rows x 4 chunks per ds_read_b128) are then free of
-// bank conflicts on gfx950, which 144 B padded rows are not (measured with the
-// LDS bank-conflict counters). The [j][s] arrays keep 80 B rows (their 2-byte
-// transposing stores are conflict-free there and conflict at every pitch that
-// frees their loads).
+// LDS layouts. Every operand array is [token][64 channels] with unpadded
+// 128 B rows whose 16 B chunks are XOR-swizzled by the row (chunk c of row r
+// sits at c ^ (r & 7)): the MFMA operand loads (16 rows x 4 chunks per
+// ds_read_b128) are then free of bank conflicts on gfx950, which 144 B padded
+// rows are not (measured with the LDS bank-conflict counters). The state
+// waves' transposed 16-token operands come from the same arrays through the
+// LDS transpose reads (ld_tr), so the operand waves store each value once, as
+// 8-byte row stores (they used to store B~^T, K~^T and v^T again, transposed,
+// with 2-byte stores).
 constexpr int kPR = kHead;  // [row][64] arrays: 128 B rows, chunk-swizzled
 // element offset of key-position element e (0..63) of row r of a [row][64] array
 __device__ __forceinline__ int rk_off(int r, int e) {
   return r * kPR + ((((e >> 3) ^ r) & 7) << 3) + (e & 7);
 }
-constexpr int kPQ = 2 * kSub + 8;  // [row][4 token groups][8] arrays (80 B rows)
 constexpr int kPG = kHead + 4;     // gam rows (floats)
 
 // Position of key row j in the [t][.] operand arrays. Key rows of the 32-row
@@ -80,26 +82,37 @@ __device__ __forceinline__ int key_pos(int j) {
   return 32 * kb + 8 * ((jj >> 2) & 3) + 4 * (jj >> 4) + (jj & 3);
 }
 
-// One sub-chunk's operands.
+// One sub-chunk's operands, every array row-major [token][channel]. The state
+// waves read the transposed 16-token operands (B~^T, K~^T, v^T) straight from
+// them with the LDS transpose reads, so nothing is stored twice.
 struct __align__(16) Slot {
   uint16_t A[2][kSub * kPR];    // A^ hi/lo [t][key_pos]
   uint16_t R[2][kSub * kPR];    // R^ hi/lo [t][key_pos]
-  // [j][s]-ordered 16-token operands: row j, token group q = s / 4 holds
-  // the 8 bf16 {hi(s = 4q..4q+3), lo(s = 4q..4q+3)}, one MFMA operand tuple.
-  uint16_t BT[kHead * kPQ];     // B~^T
-  uint16_t KT[kHead * kPQ];     // K~^T
-  uint16_t VT[kHead * kPQ];     // v^T [i][s], exact bf16, stored twice {v, v}
+  uint16_t B[2][kSub * kPR];    // B~ hi/lo [s][key_pos]
+  uint16_t K[2][kSub * kPR];    // K~ hi/lo [s][key_pos]
+  uint16_t V[kSub * kPR];       // v [s][value column], exact bf16 (natural order)
   uint4 M[4][kWave];            // T, L_ak, M_rb, M_rk as {hi, lo} in A-operand lane order
   float gam[kSub][kPG];         // e^{G_t}; row 15 is the sub-chunk's decay
 };
 
 struct __align__(16) Shared {
   Slot slot[kRing];
-  uint16_t Bs[2][2][kSub * kPR];  // B~ hi/lo [s][key_pos] of two sub-chunks
-  uint16_t Ks[2][2][kSub * kPR];  // K~ hi/lo [s][key_pos]
   float4 Lf[2][kWave];            // L_ab in fp32, A-operand lane order
   float4 sink[kWave];             // fp32 copies of the other scores (unused)
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// LDS transpose read (ds_read_b64_tr_b16). Inside each 16-lane group, lane
+// lam reads the 4 consecutive bf16 at its address, D[lam][0..3], and receives
+// D[4 j + lam / 4][lam % 4] as element j. A lane that reads row r0 + lam / 4
+// of a row-major [row][col] array at column c0 + 4 (lam % 4) therefore gets
+// column c0 + lam at rows r0 .. r0 + 3: a 16-row fragment of the transpose.
+__device__ __forceinline__ uint2 ld_tr(const uint16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
 
 // x = hi + lo: hi = bf16(x) and lo = bf16(x - hi) (the difference is exact in
 // fp32), both rounded to nearest even; |x - hi - lo| <= 2^-18 |x|. Two values
@@ -201,10 +214,6 @@ template <int N>
 __device__ __forceinline__ float elem(const uint32_t (&x)[N], int m) {
   return (m & 1) ? bf16_hi(x[m >> 1]) : bf16_lo(x[m >> 1]);
 }
-template <int N>
-__device__ __forceinline__ uint16_t elem_bits(const uint32_t (&x)[N], int m) {
-  return static_cast<uint16_t>((m & 1) ? (x[m >> 1] >> 16) : x[m >> 1]);
-}
 
 // kChan / 2 packed pairs -> an 8- or 4-byte LDS store
 template <int N>
@@ -263,20 +272,11 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
   st_pairs(&S.A[1][ro], al);
   st_pairs(&S.R[0][ro], rh);
   st_pairs(&S.R[1][ro], rl);
-  st_pairs(&sm.Bs[j & 1][0][ro], bh);
-  st_pairs(&sm.Bs[j & 1][1][ro], bl);
-  st_pairs(&sm.Ks[j & 1][0][ro], kh);
-  st_pairs(&sm.Ks[j & 1][1][ro], kl);
-#pragma unroll
-  for (int m = 0; m < kChan; ++m) {
-    const int to = (c0 + m) * kPQ + 8 * (t >> 2) + (t & 3);
-    S.BT[to] = elem_bits(bh, m);
-    S.BT[to + 4] = elem_bits(bl, m);
-    S.KT[to] = elem_bits(kh, m);
-    S.KT[to + 4] = elem_bits(kl, m);
-    S.VT[to] = elem_bits(raw.v, m);
-    S.VT[to + 4] = elem_bits(raw.v, m);
-  }
+  st_pairs(&S.B[0][ro], bh);
+  st_pairs(&S.B[1][ro], bl);
+  st_pairs(&S.K[0][ro], kh);
+  st_pairs(&S.K[1][ro], kl);
+  st_pairs(&S.V[rk_off(t, c0)], raw.v);  // value channels c0 .. c0+kChan-1
   if constexpr (kChan == 4)
     *reinterpret_cast<float4*>(&S.gam[t][c0]) = make_float4(eh[0], eh[1], eh[2], eh[3]);
   else
@@ -289,7 +289,7 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
 __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, int part) {
   Slot& S = sm.slot[j & (kRing - 1)];
   const int li = lane & 15, lg = lane >> 4;
-  const uint16_t* Y = (part & 1) ? &sm.Ks[j & 1][0][0] : &sm.Bs[j & 1][0][0];
+  const uint16_t* Y = (part & 1) ? &S.K[0][0] : &S.B[0][0];
   const uint16_t* X = (part < 2) ? &S.A[0][0] : &S.R[0][0];
   constexpr int kLo = kSub * kPR;  // hi -> lo array distance
   f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -365,15 +365,23 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
     rh[kb] = ld16(&S.R[0][off]);
     rl[kb] = ld16(&S.R[1][off]);
   }
-  const uint4 vv = ld16(&S.VT[(col0 + li) * kPQ + 8 * lg]);  // {v, v}
+  // Transposed 16-token operands by LDS transpose reads: this lane reads token
+  // row 4 lg + li / 4 at channel 4 (li % 4) of a 16-channel block and receives
+  // that block's channel li at tokens 4 lg .. 4 lg + 3.
+  const int ts = 4 * lg + (li >> 2), cq = 4 * (li & 3);
+  const uint2 v4 = ld_tr(&S.V[rk_off(ts, col0 + cq)]);
+  const uint4 vv = make_uint4(v4.x, v4.y, v4.x, v4.y);  // {v, v}: B operand [s = 4lg..][i]
   const uint4 tm = S.M[0][lane], lak = S.M[1][lane], mrb = S.M[2][lane], mrk = S.M[3][lane];
   uint4 bt[4], kt[4];
   float4 gm[4];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
-    const int jo = (16 * jb + li) * kPQ + 8 * lg;  // A operand [j = 16jb + li][s = 4lg..]
-    bt[jb] = ld16(&S.BT[jo]);
-    kt[jb] = ld16(&S.KT[jo]);
+    // A operand [j = 16jb + li][s = 4lg..4lg+3] as {hi, lo}
+    const int off = rk_off(ts, key_pos(16 * jb + cq));
+    const uint2 bh = ld_tr(&S.B[0][off]), bl = ld_tr(&S.B[1][off]);
+    const uint2 kh = ld_tr(&S.K[0][off]), kl = ld_tr(&S.K[1][off]);
+    bt[jb] = make_uint4(bh.x, bh.y, bl.x, bl.y);
+    kt[jb] = make_uint4(kh.x, kh.y, kl.x, kl.y);
     gm[jb] = *reinterpret_cast<const float4*>(&S.gam[kSub - 1][16 * jb + 4 * lg]);
   }
   // the state tiles h[2kb], h[2kb+1] as the B operand of key block kb
