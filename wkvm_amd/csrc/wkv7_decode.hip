@@ -189,12 +189,14 @@ struct BlockIn {
 };
 
 // The time-mix decode of one (row, head) in one workgroup: the WKV inputs
-// from the projection outputs (head_inputs, rounded to bf16 as the
-// element-wise kernel stores them), the state update (decode_core), and the
-// GroupNorm / bonus / gate of the bf16-rounded y (head_output). Every wave
-// derives the head's inputs on 16 lanes x 4 channels (lanes 16..63 repeat
-// the work of lanes 0..15), stages its own key rows and its copy of v in LDS,
-// and wave 0 finishes the output. Same arithmetic, in the same order, as
+// from the projection outputs (rounded to bf16 as the element-wise kernel
+// stores them), the state update (decode_core), and the GroupNorm / bonus /
+// gate of the bf16-rounded y. Lane c of every wave holds channel c of the
+// head, which is both key row c and value column c: each wave derives all 64
+// channels' inputs (head_inputs1, one channel per lane), keeps its own value
+// column's v in a register and stages its own 16 key rows in LDS; wave 0's
+// lanes then hold y, r, k and v of their channel for the output stage
+// (head_output1). Same arithmetic, in the same order, as
 // wkv7_time_mix_inputs -> wkv7_decode_slots (bf16 y) -> wkv7_time_mix_output.
 template <bool kLerpV>
 __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
@@ -203,11 +205,8 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     uint16_t* __restrict__ out, uint16_t* __restrict__ v_out) {
   __shared__ float4 s_dbkr[kHead];
   __shared__ float s_a[kHead];
-  __shared__ float s_r[kHead];             // r (unscaled), for the bonus term
-  __shared__ float s_v[kDecWaves][kHead];  // each wave's copy of v
   __shared__ float s_p[kDecWaves][kHead];
   __shared__ float s_y[kDecWaves][kHead];
-  __shared__ float s_yo[kHead];            // y rounded to bf16
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -218,34 +217,29 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
     row = row_order[pos];
     if (row < 0 || row >= B) return;
   }
-  // Lane sub holds channels 4 sub .. 4 sub + 3 of this (row, head). The row's
-  // and the head's element offsets are uniform, so every row input and
-  // parameter is addressed as a uniform base plus the lane's small offset
-  // (scalar base + vector offset; no 64-bit address per lane and input).
-  const int sub = lane & 15;
-  const int64_t ro = (row * H + head) * kHead;  // this row-head's first element
-  const int64_t po = head * kHead;              // this head's first parameter
-  const int o = 4 * sub;
-  const int pc = 4 * sub;
+  // This row-head's and this head's first elements are uniform: every input
+  // is a scalar base plus the lane's channel.
+  const int64_t ro = (row * H + head) * kHead;
+  const int64_t po = head * kHead;
   const int64_t slot = slot_ids[row];
   if (slot < 0 || slot >= num_rows) {  // a rejected row reads out zero
-    if (wave == 0 && lane < 16) {
-      st4(out + ro + o, 0.f, 0.f, 0.f, 0.f);
-      if (v_out) st4(v_out + ro + o, 0.f, 0.f, 0.f, 0.f);
+    if (wave == 0) {
+      out[ro + lane] = 0;
+      if (v_out) v_out[ro + lane] = 0;
     }
     return;
   }
 
   // The projection rows are loaded before the state rows (load counts retire
-  // in issue order), so the input arithmetic below waits for them only and
+  // in issue order), so the input arithmetic waits for them only and
   // overlaps the state stream.
-  const Bf4 rb = ld4(in.r + ro + o), kb = ld4(in.k + ro + o), vb = ld4(in.v + ro + o),
-            wlb = ld4(in.w_lora + ro + o), alb = ld4(in.a_lora + ro + o);
-  const Bf4 kksb = ld4(in.k_k + po + pc), kab = ld4(in.k_a + po + pc);
-  Bf4 vlb = {}, vfb = {};
+  const uint16_t rb = in.r[ro + lane], kb = in.k[ro + lane], vb = in.v[ro + lane],
+                 wlb = in.w_lora[ro + lane], alb = in.a_lora[ro + lane],
+                 kkb = in.k_k[po + lane], kab = in.k_a[po + lane];
+  uint16_t vlb = 0, vfb = 0;
   if (kLerpV) {
-    vlb = ld4(in.v_lora + ro + o);
-    vfb = ld4(in.v_first + ro + o);
+    vlb = in.v_lora[ro + lane];
+    vfb = in.v_first[ro + lane];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -254,72 +248,29 @@ __global__ __launch_bounds__(kWave * kDecWaves, 8) void decode_block_kernel(
 #pragma unroll
   for (int j = 0; j < kRowsPerWave; ++j) h[j] = __builtin_nontemporal_load(hp + j * kHead);
 
-  float rr[4], k[4], v[4], wl[4], al[4], kks[4], ka[4], vl[4] = {}, vf[4] = {};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    rr[e] = el(rb, e);
-    k[e] = el(kb, e);
-    v[e] = el(vb, e);
-    wl[e] = el(wlb, e);
-    al[e] = el(alb, e);
-    kks[e] = el(kksb, e);
-    ka[e] = el(kab, e);
-    if (kLerpV) {
-      vl[e] = el(vlb, e);
-      vf[e] = el(vfb, e);
-    }
-  }
-  float wv[4], kv[4], vv[4], av[4], bv[4];
-  head_inputs(k, v, wl, al, kks, ka, kLerpV, vl, vf, wv, kv, vv, av, bv);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    wv[e] = round_bf16(wv[e]);
-    kv[e] = round_bf16(kv[e]);
-    vv[e] = round_bf16(vv[e]);
-    av[e] = round_bf16(av[e]);
-    bv[e] = round_bf16(bv[e]);
-  }
-  if (lane < 16) {
-    if ((sub >> 2) == wave) {  // this wave's key rows 4 sub .. 4 sub + 3
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s_dbkr[4 * sub + e] = make_float4(expf(wv[e]), bv[e], kv[e], rr[e] * scale);
-        s_a[4 * sub + e] = av[e];
-        s_r[4 * sub + e] = rr[e];
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s_v[wave][4 * sub + e] = vv[e];
+  float wv, kv, vv, av, bv;
+  head_inputs1(bf16_to_f32(kb), bf16_to_f32(vb), bf16_to_f32(wlb), bf16_to_f32(alb),
+               bf16_to_f32(kkb), bf16_to_f32(kab), kLerpV, bf16_to_f32(vlb), bf16_to_f32(vfb),
+               wv, kv, vv, av, bv);
+  wv = round_bf16(wv);
+  kv = round_bf16(kv);
+  vv = round_bf16(vv);
+  av = round_bf16(av);
+  bv = round_bf16(bv);
+  const float rr = bf16_to_f32(rb);
+  if ((lane >> 4) == wave) {  // this wave's key rows 16 wave .. 16 wave + 15
+    s_dbkr[lane] = make_float4(expf(wv), bv, kv, rr * scale);
+    s_a[lane] = av;
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const float vi = s_v[wave][lane];
-  const float yi = decode_core<true>(hp, h, lane, wave, s_dbkr, s_a, s_p, s_y, vi);
+  const float yi = decode_core<true>(hp, h, lane, wave, s_dbkr, s_a, s_p, s_y, vv);
   if (wave == 0) {
-    // y goes to the output stage rounded to bf16, as the unfused path stores
-    // it; r, k and v come back from LDS (every wave's rows are visible after
-    // decode_core's barriers), so nothing stays live across the update
-    s_yo[lane] = round_bf16(yi);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    float y4[4], r4[4], k4[4], v4[4], g[4], rk[4], lw[4], lb[4], ov[4];
-    const Bf4 gb = ld4(in.g + ro + o), rkb = ld4(in.r_k + po + pc), lwb = ld4(in.ln_w + po + pc),
-              lbb = ld4(in.ln_b + po + pc);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int c = 4 * sub + e;
-      y4[e] = s_yo[c];
-      r4[e] = s_r[c];
-      k4[e] = s_dbkr[c].z;
-      v4[e] = s_v[0][c];
-      g[e] = el(gb, e);
-      rk[e] = el(rkb, e);
-      lw[e] = el(lwb, e);
-      lb[e] = el(lbb, e);
-    }
-    head_output(y4, r4, k4, v4, g, rk, lw, lb, eps, ov);
-    if (lane < 16) {
-      st4(out + ro + o, ov[0], ov[1], ov[2], ov[3]);
-      if (v_out) st4(v_out + ro + o, v4[0], v4[1], v4[2], v4[3]);
-    }
+    // y goes to the output stage rounded to bf16, as the unfused path stores it
+    const float o = head_output1(round_bf16(yi), rr, kv, vv, bf16_to_f32(in.g[ro + lane]),
+                                 bf16_to_f32(in.r_k[po + lane]), bf16_to_f32(in.ln_w[po + lane]),
+                                 bf16_to_f32(in.ln_b[po + lane]), eps);
+    out[ro + lane] = f32_to_bf16(o);
+    if (v_out) v_out[ro + lane] = f32_to_bf16(vv);
   }
 }
 

@@ -113,4 +113,81 @@ __device__ __forceinline__ void head_output(const float (&yin)[4], const float (
   for (int e = 0; e < 4; ++e) o[e] = fmaf(bonus, v[e], fmaf(y[e] * rstd, lw[e], lb[e])) * g[e];
 }
 
+// -- one channel per lane over a whole wave (lane c = channel c of the head) --
+// The same values as head_inputs / head_output, bit for bit: every reduction
+// is rebuilt in the 4-channel layout's order. The 4-channel lane `sub` holds
+// channels 4 sub .. 4 sub + 3 and runs a sequential chain over them; here the
+// four lanes of a quad are those channels, each gathers the quad's values by
+// DPP and runs the same chain. row_sum16's butterfly over subs (xor 1, 2, 4,
+// 8) is the lane butterfly xor 4, 8, 16, 32, with the same operand order.
+
+// Lane E of this lane's quad, on every lane of the quad.
+template <int E>
+__device__ __forceinline__ float quad_get(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), E | (E << 2) | (E << 4) | (E << 6),
+                                                 0xf, 0xf, false));
+}
+
+// row_sum16 of the per-sub partials (each equal on its quad's lanes).
+__device__ __forceinline__ float sub_sum64(float x) {
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ void head_inputs1(float k, float v, float wl, float al, float kks,
+                                             float ka, bool lerp_v, float vl, float vf, float& w,
+                                             float& ko, float& vo, float& a, float& b) {
+  const float kk = k * kks;
+  const float sa = sigmoidf(al);
+  const float q0 = quad_get<0>(kk), q1 = quad_get<1>(kk), q2 = quad_get<2>(kk),
+              q3 = quad_get<3>(kk);
+  float ssq = 0.f;
+  ssq = fmaf(q0, q0, ssq);
+  ssq = fmaf(q1, q1, ssq);
+  ssq = fmaf(q2, q2, ssq);
+  ssq = fmaf(q3, q3, ssq);
+  ssq = sub_sum64(ssq);
+  const float inv = 1.f / fmaxf(sqrtf(ssq), 1e-12f);
+  const float n = kk * inv;
+  w = -kDecayScale * sigmoidf(wl);
+  ko = k * fmaf(sa - 1.f, ka, 1.f);
+  a = -n;
+  b = n * sa;
+  vo = lerp_v ? fmaf(vf - v, sigmoidf(vl), v) : v;
+}
+
+__device__ __forceinline__ float head_output1(float y, float r, float k, float v, float g,
+                                              float rk, float lw, float lb, float eps) {
+  const float rkp = r * k;
+  const float y0 = quad_get<0>(y), y1 = quad_get<1>(y), y2 = quad_get<2>(y), y3 = quad_get<3>(y);
+  const float p0 = quad_get<0>(rkp), p1 = quad_get<1>(rkp), p2 = quad_get<2>(rkp),
+              p3 = quad_get<3>(rkp);
+  const float c0 = quad_get<0>(rk), c1 = quad_get<1>(rk), c2 = quad_get<2>(rk),
+              c3 = quad_get<3>(rk);
+  float sum = 0.f, bonus = 0.f;
+  sum += y0;
+  bonus = fmaf(p0, c0, bonus);
+  sum += y1;
+  bonus = fmaf(p1, c1, bonus);
+  sum += y2;
+  bonus = fmaf(p2, c2, bonus);
+  sum += y3;
+  bonus = fmaf(p3, c3, bonus);
+  const float mean = sub_sum64(sum) * (1.f / kHead);
+  bonus = sub_sum64(bonus);
+  const float yc = y - mean;
+  const float s0 = quad_get<0>(yc), s1 = quad_get<1>(yc), s2 = quad_get<2>(yc),
+              s3 = quad_get<3>(yc);
+  float sq = 0.f;
+  sq = fmaf(s0, s0, sq);
+  sq = fmaf(s1, s1, sq);
+  sq = fmaf(s2, s2, sq);
+  sq = fmaf(s3, s3, sq);
+  const float rstd = 1.f / sqrtf(fmaf(sub_sum64(sq), 1.f / kHead, eps));  // biased variance
+  return fmaf(bonus, v, fmaf(yc * rstd, lw, lb)) * g;
+}
+
 }  // namespace wkv7
