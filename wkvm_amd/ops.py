@@ -954,11 +954,16 @@ def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqle
 def fused_recurrent_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=None,
                           output_final_state: bool = True, cu_seqlens=None,
                           head_first: bool = False):
-    """fla-signature recurrent WKV7 (the reference's decode / T < 64 path).
+    """fla-signature recurrent WKV7 (the reference's decode / T < 64 path,
+    wkvm/models/rwkv7.py:108-111).
 
     Tensors ``[B, T, H, 64]`` bf16 (``w`` log-decay); ``initial_state``
     ``[N, H, 64, 64]`` fp32 with N = B, or the number of packed sequences when
-    ``cu_seqlens`` is given. Returns ``(o, final_state)``.
+    ``cu_seqlens`` is given (a host sequence or a device tensor of any integer
+    dtype). Returns ``(o, final_state)``; ``initial_state`` is not modified.
+    One token per sequence runs ``wkv7_decode_into``: the state is read from
+    ``initial_state`` and written to a new ``final_state`` (or not at all when
+    ``output_final_state`` is False), with no copy.
     """
     return _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
                    head_first)
