@@ -2,18 +2,20 @@
 //
 // The pool tensors are layer-major ([L, S+1, ...] for wkv, [L, 2, S+1, D] for
 // the token-shift family), so one slot is `outer` strided rows of `row_bytes`
-// contiguous bytes. Work is cut into 16 KiB tiles of one row; each thread moves
-// U vectors of the widest type the pointers, strides and row size allow.
-// Pure HBM streaming: no LDS, loads of one tile are all issued before its
-// stores, and both carry non-temporal hints (5 % faster on a 7B fork round than
-// plain accesses; deeper unrolling is slower).
+// contiguous bytes. Work is cut into 16 KiB tiles of one row; each of a block's
+// 512 threads moves 2 vectors of the widest type the pointers, strides and row
+// size allow. Pure HBM streaming: no LDS, loads of one tile are all issued
+// before its stores, and both carry non-temporal hints (5 % faster on a 7B fork
+// round than plain accesses). On that round 512 x 2 runs 3 % faster than
+// 256 x 4; deeper unrolling, 768- or 1024-thread blocks and a persistent grid
+// are all slower.
 #include "wkv7_common.h"
 
 namespace wkv7 {
 namespace {
 
-constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 4;
+constexpr int kCopyThreads = 512;
+constexpr int kCopyUnroll = 2;
 
 struct RowMap {
   char* dst;
