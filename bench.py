@@ -21,7 +21,6 @@ reads and writes all 24 layers' distinct slot state (3 GiB, far beyond the
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import re
@@ -244,8 +243,6 @@ def bench_proj(torch, dev, args):
     24 layers' distinct weights and inputs (0.9 GB, beyond the 256 MB
     Infinity Cache); algorithmic bytes = weights + the distinct x rows + the
     outputs."""
-    import ctypes
-
     from wkvm_amd import _lib
     from wkvm_amd.layout import RWKV7StateLayout
     from wkvm_amd.timemix import RWKV7TimeMix

@@ -8,7 +8,6 @@ float64 tanh / sigmoid of the exact sum.
 
 import math
 
-import numpy as np
 import pytest
 import torch
 

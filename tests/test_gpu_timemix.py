@@ -24,7 +24,6 @@ import numpy as np
 import pytest
 import torch
 
-import oracle as O
 from oracle import timemix as TM
 from tests import util as U
 from wkvm_amd import ops
