@@ -147,7 +147,9 @@ int wkv7_decode_into(const float *state_in, int64_t in_rows, const int32_t *in_i
  *                 compute units with the least idle tail; results do not
  *                 depend on it
  *   r..b          [total_tokens, H, 64] bf16, 16-byte aligned (else WKV7_ERR_SHAPE)
- *   y             [total_tokens, H, 64], dtype per y_dtype
+ *   y             [total_tokens, H, 64], dtype per y_dtype; 8-byte aligned for
+ *                 bf16, 16-byte for fp32 (whole rows are stored as vectors;
+ *                 else WKV7_ERR_SHAPE)
  *
  * Decay range: the chunked form scales operands by exp(+-G) with G a sum of
  * up to 16 consecutive log-decays, so every w must be >= -5 (exp(80) is
@@ -181,7 +183,7 @@ int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
  * wkv7_prefill_varlen, n_primary + 1 entries); run n_primary + i takes tokens
  * [cu_alt[2i], cu_alt[2i+1]) of the same inputs. run_flags [nseq] (device,
  * WKV7_RUN_* bits, NULL = all 0) select the initial state, zero k and v, and
- * redirect y to y_alt (same shape and dtype as y) and the state to
+ * redirect y to y_alt (same shape, dtype and alignment as y) and the state to
  * state_alt [alt_rows, H, 64, 64] fp32. A run's rows must be distinct from
  * every other run's.
  */

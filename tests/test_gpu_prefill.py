@@ -183,6 +183,10 @@ def test_prefill_argument_errors(dev):
         ops.wkv7_prefill_varlen(pool, [1, 1], [0, 4, 10], *vecs)
     with pytest.raises(ValueError, match="bfloat16"):
         ops.wkv7_prefill_varlen(pool, [1, 2], [0, 4, 10], *(x.float() for x in vecs))
+    # y rows are stored as vectors: a contiguous out view 2 bytes off alignment is refused
+    skew = torch.empty(10 * 2 * 64 + 1, dtype=torch.bfloat16, device=dev)[1:].view(10, 2, 64)
+    with pytest.raises(ValueError, match="aligned"):
+        ops.wkv7_prefill_varlen(pool, [1, 2], [0, 4, 10], *vecs, out=skew)
 
 
 def test_mixed_step_equals_separate_calls(dev):

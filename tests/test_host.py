@@ -312,6 +312,17 @@ def test_segment_entry_points_reject_bad_arguments():
                                  None, None, 2, None, 0, None, None) == E_SHAPE
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 0, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
                                  0, None, 0, None, None) == 0
+    # y and y_alt are stored as whole-row vectors: 8-byte (bf16) / 16-byte (fp32) aligned
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 4, 0, 0, 1.0, None,
+                                 None, 2, None, 0, None, None) == E_SHAPE
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 8, 1, 0, 1.0, None,
+                                 None, 2, None, 0, None, None) == E_SHAPE
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None,
+                                 None, 2, None, 0, p + 2, None) == E_SHAPE
+    assert lib.wkv7_prefill_varlen(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 2, 0, 0, 1.0,
+                                   None) == E_SHAPE
+    assert lib.wkv7_prefill_varlen(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 8, 1, 0, 1.0,
+                                   None) == E_SHAPE
     # chain: segments without their tables; misaligned hin
     assert lib.wkv7_segment_chain(p, 4, 2, None, 0, p, 1, None, 1, p, None) == E_ARG
     assert lib.wkv7_segment_chain(p, 4, 2, p, 2, p, 1, p, 1, p + 4, None) == E_SHAPE

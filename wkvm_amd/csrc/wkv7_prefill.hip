@@ -95,10 +95,17 @@ struct __align__(16) Slot {
   float gam[kSub][kPG];         // e^{G_t}; row 15 is the sub-chunk's decay
 };
 
+// y of a sub-chunk staged for the score waves' row stores: [token][64 values]
+// rows padded by 8 bytes (bf16) or 16 bytes (fp32) so the state waves' four
+// lane groups write different banks.
+constexpr int kYRowB = kHead * 2 + 8;   // bf16 row pitch in bytes
+constexpr int kYRowF = kHead * 4 + 16;  // fp32 row pitch in bytes
+
 struct __align__(16) Shared {
   Slot slot[kRing];
   float4 Lf[2][kWave];            // L_ab in fp32, A-operand lane order
   float4 sink[kWave];             // fp32 copies of the other scores (unused)
+  unsigned char ys[2][kSub * kYRowF];  // y of sub-chunks k (state waves) and k-1 (score waves)
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -425,36 +432,43 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   return Z;
 }
 
+// The state wave's y of sub-chunk j (tokens 4lg..4lg+3, value column
+// 16 wave + li) into the staging rows, rounded as the output dtype.
 template <bool kF32Out>
-__device__ __forceinline__ void store_y(void* y, const f32x4& Z, int64_t j, const SeqGeom& g,
-                                        int lane, int wave) {
+__device__ __forceinline__ void stage_y(Shared& sm, const f32x4& Z, int64_t j, int lane,
+                                        int wave) {
   const int li = lane & 15, lg = lane >> 4;
-  const int64_t tok0 = g.t_beg + kSub * j + 4 * lg;
-  const int64_t yo = tok0 * g.tstride + g.hoff + kSub * wave + li;
-  if (g.t_beg + kSub * (j + 1) <= g.t_end) {  // uniform: the whole sub-chunk is real
-    if (kF32Out) {
-      float* yp = static_cast<float*>(y) + yo;
+  unsigned char* ys = sm.ys[j & 1];
+  const int col = kSub * wave + li;
+  if constexpr (kF32Out) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) yp[r * g.tstride] = Z[r];
-    } else {
-      uint16_t* yp = static_cast<uint16_t*>(y) + yo;
-      const uint32_t p01 = pack_bf16(Z[0], Z[1]), p23 = pack_bf16(Z[2], Z[3]);
-      yp[0] = static_cast<uint16_t>(p01);
-      yp[g.tstride] = static_cast<uint16_t>(p01 >> 16);
-      yp[2 * g.tstride] = static_cast<uint16_t>(p23);
-      yp[3 * g.tstride] = static_cast<uint16_t>(p23 >> 16);
-    }
-    return;
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float*>(ys + (4 * lg + r) * kYRowF + 4 * col) = Z[r];
+  } else {
+    const uint32_t p01 = pack_bf16(Z[0], Z[1]), p23 = pack_bf16(Z[2], Z[3]);
+    *reinterpret_cast<uint16_t*>(ys + (4 * lg + 0) * kYRowB + 2 * col) = static_cast<uint16_t>(p01);
+    *reinterpret_cast<uint16_t*>(ys + (4 * lg + 1) * kYRowB + 2 * col) = static_cast<uint16_t>(p01 >> 16);
+    *reinterpret_cast<uint16_t*>(ys + (4 * lg + 2) * kYRowB + 2 * col) = static_cast<uint16_t>(p23);
+    *reinterpret_cast<uint16_t*>(ys + (4 * lg + 3) * kYRowB + 2 * col) = static_cast<uint16_t>(p23 >> 16);
   }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (tok0 + r < g.t_end) {
-      if (kF32Out)
-        static_cast<float*>(y)[yo + r * g.tstride] = Z[r];
-      else
-        static_cast<uint16_t*>(y)[yo + r * g.tstride] = f32_to_bf16(Z[r]);
-    }
-  }
+}
+
+// Score wave p stores tokens 4p..4p+3 of sub-chunk j from the staging rows:
+// 16 lanes per token, whole 128-byte (bf16) or 256-byte (fp32) rows.
+template <bool kF32Out>
+__device__ __forceinline__ void flush_y(const Shared& sm, void* y, int64_t j, const SeqGeom& g,
+                                        int lane, int part) {
+  const int tt = 4 * part + (lane >> 4), c = 4 * (lane & 15);
+  const int64_t tok = g.t_beg + kSub * j + tt;
+  if (tok >= g.t_end) return;
+  const unsigned char* ys = sm.ys[j & 1];
+  const int64_t yo = tok * g.tstride + g.hoff + c;
+  if constexpr (kF32Out)
+    *reinterpret_cast<float4*>(static_cast<float*>(y) + yo) =
+        *reinterpret_cast<const float4*>(ys + tt * kYRowF + 4 * c);
+  else
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + yo) =
+        *reinterpret_cast<const uint2*>(ys + tt * kYRowB + 2 * c);
 }
 
 // Ends a pipeline tick. The scheduling fence keeps the compiler from moving
@@ -601,7 +615,6 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     const int li = lane & 15, lg = lane >> 4;
     float* hbase = ((fl & WKV7_RUN_STATE_ALT) ? runs.state_alt : wkv) +
                    (slot * H + head) * (kHead * kHead);
-    void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
     const int col0 = kSub * wave;  // this wave's value columns [col0, col0 + 16)
     // State columns of this wave as four 16x16 accumulator tiles (key blocks jb).
     f32x4 h[4];
@@ -623,7 +636,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
         stage_inverse(sm, k + 1, lane, wave);
-        store_y<kF32Out>(yb, yv, k, g, lane, wave);
+        stage_y<kF32Out>(sm, yv, k, lane, wave);
         end_tick();
       }
     }
@@ -635,6 +648,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   } else if (wave >= 4 + kOpWaves) {
     if (n_sub > 0) {
       const int part = wave - 4 - kOpWaves;
+      void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
       end_tick();
       stage_scores(sm, 0, lane, part);
       end_tick();
@@ -642,8 +656,10 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
       end_tick();
       for (int64_t k = 0; k < n_sub; ++k) {
         stage_scores(sm, k + 2, lane, part);
+        if (k > 0) flush_y<kF32Out>(sm, yb, k - 1, g, lane, part);
         end_tick();
       }
+      flush_y<kF32Out>(sm, yb, n_sub - 1, g, lane, part);
     }
   } else if (n_sub > 0) {
     // ---- operands ahead of the chain ----
@@ -702,6 +718,11 @@ int prefill_launch(float* wkv_layer, int64_t num_rows, int32_t H, const int32_t*
   return launch_status();
 }
 
+// y rows are stored as 8-byte (bf16) or 16-byte (fp32) vectors
+bool y_aligned(const void* y, int32_t y_dtype) {
+  return (reinterpret_cast<uintptr_t>(y) & (y_dtype == WKV7_Y_F32 ? 15u : 7u)) == 0;
+}
+
 bool inputs_aligned(const uint16_t* r, const uint16_t* w, const uint16_t* k, const uint16_t* v,
                     const uint16_t* a, const uint16_t* b) {
   // inputs are read as 16-byte vectors
@@ -724,7 +745,7 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
   if (nseq == 0) return WKV7_OK;
   if (!wkv_layer || !slot_ids || !cu_seqlens) return WKV7_ERR_ARG;
   if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
-  if (!inputs_aligned(r, w, k, v, a, b)) return WKV7_ERR_SHAPE;
+  if (!inputs_aligned(r, w, k, v, a, b) || !y_aligned(y, y_dtype)) return WKV7_ERR_SHAPE;
   const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr};
   return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
                         total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,
@@ -748,7 +769,9 @@ extern "C" int wkv7_prefill_runs(float* wkv_layer, int64_t num_rows, int32_t H,
   if (n_primary < nseq && !cu_alt) return WKV7_ERR_ARG;
   if (alt_rows > 0 && !state_alt) return WKV7_ERR_ARG;
   if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
-  if (!inputs_aligned(r, w, k, v, a, b)) return WKV7_ERR_SHAPE;
+  if (!inputs_aligned(r, w, k, v, a, b) || !y_aligned(y, y_dtype) ||
+      (y_alt && !y_aligned(y_alt, y_dtype)))
+    return WKV7_ERR_SHAPE;
   const Runs runs{run_flags, cu_alt, n_primary, state_alt, alt_rows, y_alt ? y_alt : y};
   return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
                         total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,

@@ -305,6 +305,9 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
             raise ValueError("seq_order must be a device int32 tensor of nseq entries")
     code = _y_code(out.dtype if out is not None else out_dtype)
     y = _out(out, (T, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
+    if y.data_ptr() % (16 if y.dtype == torch.float32 else 8):
+        raise ValueError("out must be 8-byte aligned (bf16) or 16-byte aligned (fp32): the "
+                         "kernel stores whole rows as vectors")
     if nseq == 0:
         return y
     rc = _lib.load().wkv7_prefill_varlen(wkv_layer.data_ptr(), rows, H, ids.data_ptr(),
