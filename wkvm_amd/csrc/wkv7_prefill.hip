@@ -28,10 +28,14 @@
 // Sub-chunk j lives in ring slot j % 4 from tick j-3 to tick j; its inputs
 // are loaded two ticks before they are used.
 //
-// Precision: every MFMA operand that is not an exact bf16 input is split into
-// bf16 hi + lo parts and a product is formed as hi*hi + hi*lo + lo*hi with
-// fp32 accumulation (~2^-16 relative per product); products with the exact
-// bf16 v need two MFMAs. T is solved in fp32. Operand layouts below
+// Precision: MFMA operands that are not exact bf16 inputs are split into bf16
+// hi + lo parts, a product formed as hi*hi + hi*lo + lo*hi with fp32
+// accumulation (~2^-16 relative per product), except three that enter as one
+// bf16 each: A^, T (solved in fp32, then rounded) and h in the A^ h product.
+// Those cost ~2^-9 relative on P only; over 4096 tokens the worst final state
+// of a config-2 batch is 2.8e-4 relative L2 from the all-split form (y 1.8e-4)
+// and ~7 % of the time. Products with the exact bf16 v need one MFMA per term
+// pair. Operand layouts below
 // (v_mfma_f32_16x16x32_bf16, lane l, li = l%16, lg = l/16): A lane holds
 // A[li][8lg..8lg+7] of a 32-wide k block, B lane holds B[8lg..8lg+7][li], the
 // accumulator holds D[4lg..4lg+3][li]. Contractions over 16 tokens put
@@ -86,7 +90,7 @@ __device__ __forceinline__ int key_pos(int j) {
 // waves read the transposed 16-token operands (B~^T, K~^T, v^T) straight from
 // them with the LDS transpose reads, so nothing is stored twice.
 struct __align__(16) Slot {
-  uint16_t A[2][kSub * kPR];    // A^ hi/lo [t][key_pos]
+  uint16_t A[kSub * kPR];       // A^ as one bf16 [t][key_pos]
   uint16_t R[2][kSub * kPR];    // R^ hi/lo [t][key_pos]
   uint16_t B[2][kSub * kPR];    // B~ hi/lo [s][key_pos]
   uint16_t K[2][kSub * kPR];    // K~ hi/lo [s][key_pos]
@@ -264,10 +268,10 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
     B_[m] = elem(bv, m) * ie;
     K_[m] = elem(kv, m) * ie;
   }
-  uint32_t ah[P], al[P], rh[P], rl[P], bh[P], bl[P], kh[P], kl[P];
+  uint32_t ah[P], rh[P], rl[P], bh[P], bl[P], kh[P], kl[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    split2(A_[2 * i], A_[2 * i + 1], ah[i], al[i]);
+    ah[i] = pack_bf16(A_[2 * i], A_[2 * i + 1]);
     split2(R_[2 * i], R_[2 * i + 1], rh[i], rl[i]);
     split2(B_[2 * i], B_[2 * i + 1], bh[i], bl[i]);
     split2(K_[2 * i], K_[2 * i + 1], kh[i], kl[i]);
@@ -275,8 +279,7 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
 
   const int c0 = kChan * (4 * part + cg);  // key channels c0 .. c0+kChan-1 (consecutive key_pos)
   const int ro = rk_off(t, key_pos(c0));  // kChan consecutive elements inside one chunk
-  st_pairs(&S.A[0][ro], ah);
-  st_pairs(&S.A[1][ro], al);
+  st_pairs(&S.A[ro], ah);
   st_pairs(&S.R[0][ro], rh);
   st_pairs(&S.R[1][ro], rl);
   st_pairs(&S.B[0][ro], bh);
@@ -292,18 +295,24 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
 
 // Score matrix `part` of sub-chunk j (0: L_ab, 1: L_ak, 2: M_rb, 3: M_rk) as
 // the transposed product Y X^T, whose accumulator is the matrix in A-operand
-// lane order.
-__device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, int part) {
+// lane order. X is A^ (one bf16) for the L matrices and the split R^ for M.
+template <int part>
+__device__ __forceinline__ void stage_scores_of(Shared& sm, int64_t j, int lane) {
   Slot& S = sm.slot[j & (kRing - 1)];
   const int li = lane & 15, lg = lane >> 4;
   const uint16_t* Y = (part & 1) ? &S.K[0][0] : &S.B[0][0];
-  const uint16_t* X = (part < 2) ? &S.A[0][0] : &S.R[0][0];
   constexpr int kLo = kSub * kPR;  // hi -> lo array distance
   f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int off = rk_off(li, 32 * kb + 8 * lg);
-    d = mma32x3(ld16(Y + off), ld16(Y + kLo + off), ld16(X + off), ld16(X + kLo + off), d);
+    const uint4 yh = ld16(Y + off);
+    if constexpr (part < 2) {
+      d = mma32(ld16(Y + kLo + off), ld16(&S.A[off]), d);  // (yh + yl) A^
+      d = mma32(yh, ld16(&S.A[off]), d);
+    } else {
+      d = mma32x3(yh, ld16(Y + kLo + off), ld16(&S.R[0][off]), ld16(&S.R[1][off]), d);
+    }
   }
   // d[r] = M[t = li][s = 4lg + r]; L_* keep s < t, M_* keep s <= t
   const int lim = li + (part >> 1);
@@ -314,7 +323,15 @@ __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, in
   uint2 hi, lo;
   pack_split(d, hi, lo);
   S.M[part][lane] = make_uint4(hi.x, hi.y, lo.x, lo.y);  // part 0's is overwritten by T
+}
 
+__device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, int part) {
+  switch (part) {  // wave-uniform
+    case 0: stage_scores_of<0>(sm, j, lane); break;
+    case 1: stage_scores_of<1>(sm, j, lane); break;
+    case 2: stage_scores_of<2>(sm, j, lane); break;
+    default: stage_scores_of<3>(sm, j, lane); break;
+  }
 }
 
 // One forward-substitution step: every lane of a 16-lane DPP row receives
@@ -345,12 +362,12 @@ __device__ __forceinline__ void stage_inverse(Shared& sm, int64_t j, int lane, i
   }
   float acc = (tq == 4 * part + cl) ? 1.f : 0.f;
   subst_steps<0>(acc, Lr);
-  uint32_t hi, lo;
-  split2(acc, 0.f, hi, lo);
-  // T[tq][4 part + cl] sits in lane tq + 16 part, element cl of the A operand
+  const uint16_t t16 = static_cast<uint16_t>(pack_bf16(acc, 0.f));
+  // T[tq][4 part + cl] sits in lane tq + 16 part, element cl of the A operand,
+  // once in each half (P = T X takes X's hi and lo halves in one product)
   uint16_t* Tm = reinterpret_cast<uint16_t*>(&S.M[0][tq + 16 * part]);
-  Tm[cl] = static_cast<uint16_t>(hi);
-  Tm[4 + cl] = static_cast<uint16_t>(lo);
+  Tm[cl] = t16;
+  Tm[4 + cl] = t16;
 }
 
 // State chain of sub-chunk j for value columns [16 wave, 16 wave + 16);
@@ -363,12 +380,11 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   const Slot& S = sm.slot[j & (kRing - 1)];
   const int li = lane & 15, lg = lane >> 4;
   const int col0 = kSub * wave;
-  uint4 ah[2], al[2], rh[2], rl[2];
+  uint4 ah[2], rh[2], rl[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int off = rk_off(li, 32 * kb + 8 * lg);
-    ah[kb] = ld16(&S.A[0][off]);
-    al[kb] = ld16(&S.A[1][off]);
+    ah[kb] = ld16(&S.A[off]);
     rh[kb] = ld16(&S.R[0][off]);
     rl[kb] = ld16(&S.R[1][off]);
   }
@@ -406,13 +422,12 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   f32x4 Z = mma32(mrk, vv, zero);  // M_rk V
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    X = mma32x3(ah[kb], al[kb], hbh[kb], hbl[kb], X);  // + A^ h
+    X = mma32(ah[kb], hbh[kb], X);  // + A^ h (A^ and h as one bf16 each)
     Z = mma32x3(rh[kb], rl[kb], hbh[kb], hbl[kb], Z);  // + R^ h
   }
   uint2 xh, xl;
   pack_split(X, xh, xl);
-  f32x4 P = mma32(tm, make_uint4(xh.x, xh.y, 0u, 0u), zero);  // th xh (+ tl 0)
-  P = mma32(tm, make_uint4(xl.x, xl.y, xh.x, xh.y), P);     // + th xl + tl xh
+  const f32x4 P = mma32(tm, make_uint4(xh.x, xh.y, xl.x, xl.y), zero);  // T xh + T xl
   uint2 ph, pl;
   pack_split(P, ph, pl);
   const uint4 pp = make_uint4(pl.x, pl.y, ph.x, ph.y);  // {pl, ph}
