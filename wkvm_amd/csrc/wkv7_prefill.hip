@@ -19,10 +19,13 @@
 //
 // Schedule: a four-deep software pipeline over sub-chunks, one workgroup
 // barrier per tick. In tick k four state waves run sub-chunk k's state step
-// (the products above, 16 value columns each) and
+// (the products above, 16 value columns each; y goes to an LDS staging
+// buffer) and
 //   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
 // while eight more waves prepare the sub-chunks further ahead:
-//   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave
+//   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave; they
+//                              also store sub-chunk k-1's y from the staging
+//                              buffer as whole rows
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
 //                              per wave
 // Sub-chunk j lives in ring slot j % 4 from tick j-3 to tick j; its inputs
