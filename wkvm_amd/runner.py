@@ -126,10 +126,11 @@ class WKV7Runner:
 
         With ``concurrent`` the decode launches go to a side stream, forked
         from and joined back into the current stream, so the HBM-bound decode
-        kernels can run on the compute units the latency-bound prefill leaves
-        idle (its ragged tail, its spare wave slots); on config 4 that saves
-        1.7 % of the step. The two touch disjoint slots, so results are
-        identical either way."""
+        kernels can run on the compute units the prefill's ragged tail leaves
+        idle. A prefill workgroup now fills its compute unit's registers, so
+        on config 4 this equals one stream (17.72 ms against 17.72-17.76 ms
+        for either serial order, medians of 16 interleaved steps). The two
+        touch disjoint slots, so results are identical either way."""
         self._check_layers(decode_inputs)
         self._check_layers(prefill_inputs)
         if len(prefill_lens) != len(prefill_batch):
