@@ -342,3 +342,69 @@ def test_rejected_device_ids_read_out_zero(dev):
     torch.cuda.synchronize()
     assert not torch.any(out[1]) and not torch.any(v_out[1]) and torch.any(out[0])
     assert torch.equal(blk_pool[[0, 1, 3, 5, 6]], before[[0, 1, 3, 5, 6]])
+
+
+def test_requests_in_one_batch_match_each_request_alone(dev):
+    """State isolation as the reference checks it (two requests decoded as one
+    batch give what each gives alone, tests/test_rwkv7_gpu.py:254-276), at the
+    WKV level and bit for bit: two prompts (150 and 77 tokens) prefilled through
+    WKV7Runner.prefill, then 12 decode steps with both rows in one batch, equal
+    each request run alone on a fresh bank (every step's y and the final
+    states); and a mixed step in which one request decodes while the other
+    prefills equals the two calls made separately (the reference engine's
+    decode / prefill split, engine.py:142-170)."""
+    lay = RWKV7StateLayout(n_layer=3, hidden_size=256, num_heads=4, head_dim=64, head_v_dim=64,
+                           dtype=torch.bfloat16)
+    H, L, steps = 4, 3, 12
+    gen = synthetic.make_generator(401)
+    lens = [150, 77]
+    prompts = [[synthetic.order(synthetic.wkv7_vectors((n, H, 64), gen)) for _ in range(L)]
+               for n in lens]
+    dec = [[[synthetic.order(synthetic.wkv7_vectors((1, H, 64), gen)) for _ in range(L)]
+            for _ in range(steps)] for _ in lens]
+    slots = [{"wkv": 2, "shift": 2}, {"wkv": 5, "shift": 5}]
+
+    def on_dev(layer_inputs):
+        return [[x.to(dev) for x in xs] for xs in layer_inputs]
+
+    def run(reqs):
+        bank = RWKV7StateBank(lay, num_slots=6, device=dev)
+        runner = WKV7Runner(bank, prefill_chunk=64)
+        for i in reqs:
+            runner.prefill(on_dev(prompts[i]), slots[i], out_dtype=torch.float32)
+        ys = []
+        for s in range(steps):
+            inputs = [[torch.cat([dec[i][s][layer][n] for i in reqs]).to(dev) for n in range(6)]
+                      for layer in range(L)]
+            ys.append(runner.decode_step([slots[i] for i in reqs], inputs,
+                                         out_dtype=torch.float32))
+        torch.cuda.synchronize()
+        return bank.wkv.clone(), ys
+
+    both, y_both = run([0, 1])
+    for i in (0, 1):
+        alone, y_alone = run([i])
+        sl = slots[i]["wkv"]
+        assert torch.equal(both[:, sl], alone[:, sl]), f"request {i}: final state"
+        for s in range(steps):
+            for layer in range(L):
+                assert torch.equal(y_both[s][layer][i], y_alone[s][layer][0]), (i, s, layer)
+
+    # request 0 decodes one token while request 1 prefills, in one mixed step
+    bank = RWKV7StateBank(lay, num_slots=6, device=dev)
+    runner = WKV7Runner(bank, prefill_chunk=64)
+    runner.prefill(on_dev(prompts[0]), slots[0], out_dtype=torch.float32)
+    sep = bank.wkv.clone()
+    dec_y, pre_y = runner.mixed_step([slots[0]], on_dev(dec[0][0]), [slots[1]], [lens[1]],
+                                     on_dev(prompts[1]), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    bank2 = RWKV7StateBank(lay, num_slots=6, device=dev)
+    bank2.wkv.copy_(sep)
+    runner2 = WKV7Runner(bank2, prefill_chunk=64)
+    y_dec = runner2.decode_step([slots[0]], on_dev(dec[0][0]), out_dtype=torch.float32)
+    y_pre = runner2.prefill(on_dev(prompts[1]), slots[1], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(bank.wkv, bank2.wkv)
+    for layer in range(L):
+        assert torch.equal(dec_y[layer], y_dec[layer])
+        assert torch.equal(pre_y[layer], y_pre[layer])
