@@ -408,3 +408,32 @@ def test_requests_in_one_batch_match_each_request_alone(dev):
     for layer in range(L):
         assert torch.equal(dec_y[layer], y_dec[layer])
         assert torch.equal(pre_y[layer], y_pre[layer])
+
+
+def test_cfg3_fork_then_decode_at_full_size(dev):
+    """Config 3 at its own size, one layer: 7B heads (H = 64), 1153 slot rows,
+    1024 live slots scattered over rows 1..1024. 128 seeded live slots are
+    forked into the free rows 1025..1152 (bit-exact copies), then one decode
+    step of all 1024 live slots is checked against the oracle (every live
+    slot's state and its fp32 y); the forked children keep their sources'
+    pre-step state and pad row 0 stays zero."""
+    H, S, B = 64, 1152, 1024
+    gen = synthetic.make_generator(331)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:B + 1] = synthetic.initial_states((B, H, 64, 64), gen)
+    live = synthetic.active_slots(B, B, gen)
+    src = [live[i] for i in torch.randperm(B, generator=gen)[:128].tolist()]
+    dst = list(range(B + 1, S + 1))
+    gpool = pool.to(dev)
+    del pool
+    ops.slot_copy(gpool, dst, gpool, src, slot_dim=0)
+    torch.cuda.synchronize()
+    before = gpool.cpu().numpy()
+    assert np.array_equal(before[dst], before[src])
+    vecs = synthetic.wkv7_vectors((B, H, 64), gen)
+    y = ops.wkv7_decode_slots(gpool, live, *(vecs[n].to(dev) for n in "rwkvab"),
+                              out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check_step(before, live, U.vec_bits(vecs), gpool, y)
+    assert torch.equal(gpool[dst].cpu(), torch.from_numpy(before[dst]))
+    assert not torch.any(gpool[0])
