@@ -1,6 +1,6 @@
 // Varlen WKV7 prefill over slot states: chunked scan on MFMA.
 //
-// One workgroup (12 wavefronts) walks one (sequence, head). The 64x64 fp32
+// One workgroup (16 wavefronts) walks one (sequence, head). The 64x64 fp32
 // state stays in MFMA accumulator registers for the whole sequence (state
 // wave q owns value columns [16q, 16q+16)) and touches HBM only to load the
 // slot state at the start and store it at the end.
@@ -20,9 +20,8 @@
 // Schedule: a four-deep software pipeline over sub-chunks, one workgroup
 // barrier per tick. In tick k four state waves run sub-chunk k's state step
 // (the products above, 16 value columns each; y goes to an LDS staging
-// buffer) and
+// buffer) while twelve more waves prepare the sub-chunks further ahead:
 //   inverse   (sub-chunk k+1): T = (I - L_ab)^{-1}, 4 columns per wave
-// while eight more waves prepare the sub-chunks further ahead:
 //   scores    (sub-chunk k+2): L_ab, L_ak, M_rb, M_rk, one per wave; they
 //                              also store sub-chunk k-1's y from the staging
 //                              buffer as whole rows
@@ -63,7 +62,7 @@ constexpr int kSub = 16;
 constexpr int kRing = 4;
 constexpr int kOpWaves = 4;                      // operand wavefronts
 constexpr int kChan = kHead / (4 * kOpWaves);  // key channels per operand lane
-constexpr int kThreads = kWave * (8 + kOpWaves);  // 4 state + operand + 4 score waves
+constexpr int kThreads = kWave * (12 + kOpWaves);  // 4 state + operand + 4 score + 4 inverse
 // LDS layouts. Every operand array is [token][64 channels] with unpadded
 // 128 B rows whose 16 B chunks are XOR-swizzled by the row (chunk c of row r
 // sits at c ^ (r & 7)): the MFMA operand loads (16 rows x 4 chunks per
@@ -577,13 +576,15 @@ __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const S
   if (k < n_sub) prep_tick<kMask>(sm, p1, k, ld, g, lane, part, scale);
 }
 
-// Twelve wavefronts in three kinds: waves 0-3 run the state chain (wave q
-// owns value columns [16q, 16q+16)) and T columns [4q, 4q+4) of the next
-// sub-chunk; waves 4-7 build operands (part p = wave - 4 handles key channels
-// [16p, 16p+16)); waves 8-11 compute score matrix p = wave - 8. Each SIMD
-// holds one wave of each kind, so the hardware interleaves the state chain's
-// MFMA latencies with the operand and score work. All kinds pass the same
-// sequence of barriers: three fill ticks, then one per sub-chunk.
+// Sixteen wavefronts in four kinds: waves 0-3 run the state chain (wave q
+// owns value columns [16q, 16q+16)); waves 4-7 build operands (part p =
+// wave - 4 handles key channels [16p, 16p+16)); waves 8-11 compute score
+// matrix p = wave - 8; waves 12-15 solve T columns [4p, 4p+4) of the next
+// sub-chunk, p = wave - 12. Each SIMD holds one wave of each kind, so the
+// hardware interleaves the state chain's MFMA latencies with the other work,
+// and the inverse's serial substitution chain runs beside the state chain
+// instead of after it in the same wave. All kinds pass the same sequence of
+// barriers: three fill ticks, then one per sub-chunk.
 // Per-run options of wkv7_prefill_runs (all absent for wkv7_prefill_varlen).
 // Runs [0, n_primary) take their token range from cu_seqlens; run
 // n_primary + i takes [ranges[2i], ranges[2i+1]). Flags select the initial
@@ -649,11 +650,9 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     if (n_sub > 0) {
       end_tick();  // fill ticks
       end_tick();
-      stage_inverse(sm, 0, lane, wave);
       end_tick();
       for (int64_t k = 0; k < n_sub; ++k) {
         const f32x4 yv = stage_state(sm, h, k, lane, wave);
-        stage_inverse(sm, k + 1, lane, wave);
         stage_y<kF32Out>(sm, yv, k, lane, wave);
         end_tick();
       }
@@ -663,6 +662,19 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
         hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
+  } else if (wave >= 8 + kOpWaves) {
+    // ---- T of the next sub-chunk ----
+    if (n_sub > 0) {
+      const int part = wave - 8 - kOpWaves;
+      end_tick();
+      end_tick();
+      stage_inverse(sm, 0, lane, part);
+      end_tick();
+      for (int64_t k = 0; k < n_sub; ++k) {
+        stage_inverse(sm, k + 1, lane, part);
+        end_tick();
+      }
+    }
   } else if (wave >= 4 + kOpWaves) {
     if (n_sub > 0) {
       const int part = wave - 4 - kOpWaves;
