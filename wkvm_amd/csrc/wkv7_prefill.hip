@@ -607,7 +607,10 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   __shared__ Shared sm;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform by construction; through readfirstlane the compiler knows it,
+  // so the role and score-part branches are scalar branches instead of
+  // exec-mask sequences over every body
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t pos = blockIdx.x / H;
   const int64_t head = blockIdx.x - pos * H;
   const int64_t seq = seq_order ? int64_t(seq_order[pos]) : pos;
