@@ -110,7 +110,6 @@ constexpr int kYRowF = kHead * 4 + 16;  // fp32 row pitch in bytes
 struct __align__(16) Shared {
   Slot slot[kRing];
   float4 Lf[2][kWave];            // L_ab in fp32, A-operand lane order
-  float4 sink[kWave];             // fp32 copies of the other scores (unused)
   unsigned char ys[2][kSub * kYRowF];  // y of sub-chunks k (state waves) and k-1 (score waves)
 };
 
@@ -320,11 +319,13 @@ __device__ __forceinline__ void stage_scores_of(Shared& sm, int64_t j, int lane)
   const int lim = li + (part >> 1);
 #pragma unroll
   for (int r = 0; r < 4; ++r) d[r] = (4 * lg + r < lim) ? d[r] : 0.f;
-  float4* fdst = (part == 0) ? sm.Lf[j & 1] : sm.sink;
-  fdst[lane] = make_float4(d[0], d[1], d[2], d[3]);
-  uint2 hi, lo;
-  pack_split(d, hi, lo);
-  S.M[part][lane] = make_uint4(hi.x, hi.y, lo.x, lo.y);  // part 0's is overwritten by T
+  if constexpr (part == 0) {
+    sm.Lf[j & 1][lane] = make_float4(d[0], d[1], d[2], d[3]);  // T is solved from it in fp32
+  } else {
+    uint2 hi, lo;
+    pack_split(d, hi, lo);
+    S.M[part][lane] = make_uint4(hi.x, hi.y, lo.x, lo.y);
+  }
 }
 
 __device__ __forceinline__ void stage_scores(Shared& sm, int64_t j, int lane, int part) {
