@@ -28,7 +28,10 @@
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
 //                              per wave
 // Sub-chunk j lives in ring slot j % 4 from tick j-3 to tick j; its inputs
-// are loaded two ticks before they are used.
+// are loaded two ticks before they are used, as whole 128-byte rows straight
+// into an LDS staging ring of three sub-chunks (the buffer path, every batch
+// whose input offsets fit 31 bits; one more fill tick) or into registers
+// (larger batches).
 //
 // Precision: MFMA operands that are not exact bf16 inputs are split into bf16
 // hi + lo parts, a product formed as hi*hi + hi*lo + lo*hi with fp32
@@ -111,7 +114,17 @@ struct __align__(16) Shared {
   Slot slot[kRing];
   float4 Lf[2][kWave];            // L_ab in fp32, A-operand lane order
   unsigned char ys[2][kSub * kYRowF];  // y of sub-chunks k (state waves) and k-1 (score waves)
+  uint4 inb[3][6][kSub][8];  // input rows (r, w, k, v, a, b) of three sub-chunks, 128 B each
 };
+
+typedef __attribute__((address_space(3))) uint4 lds_uint4;
+__device__ __forceinline__ uint32_t lds_addr(const uint4* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_uint4*)p));
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -234,6 +247,28 @@ __device__ __forceinline__ void st_pairs(uint16_t* p, const uint32_t (&x)[N]) {
     *reinterpret_cast<uint2*>(p) = make_uint2(x[0], x[1]);
   else
     *reinterpret_cast<uint32_t*>(p) = x[0];
+}
+
+// This lane's kChan channels of token t = lane % 16 of every input, from
+// staging slot `slot` (rows stored with their 16-byte chunks XOR-swizzled by
+// the token, see row_sources).
+__device__ __forceinline__ void read_inputs(const Shared& sm, SubIn& d, int slot, int lane,
+                                            int part) {
+  const int t = lane & 15, cg = lane >> 4;
+  const int c = 2 * part + (cg >> 1);
+  const int pos = ((c ^ (t & 7)) * 16) + (cg & 1) * 8;
+  auto rd = [&](uint32_t (&x)[kChan / 2], int input) {
+    const uint2 v = *reinterpret_cast<const uint2*>(
+        reinterpret_cast<const unsigned char*>(&sm.inb[slot][input][t][0]) + pos);
+    x[0] = v.x;
+    x[1] = v.y;
+  };
+  rd(d.r, 0);
+  rd(d.w, 1);
+  rd(d.k, 2);
+  rd(d.v, 3);
+  rd(d.a, 4);
+  rd(d.b, 5);
 }
 
 // Operands of sub-chunk j for key channels [4 kChan part, 4 kChan (part + 1)).
@@ -507,37 +542,6 @@ __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, con
   end_tick();
 }
 
-// Operand waves' input loads through one buffer resource per input, based at
-// this (sequence, head)'s first token and sized to the sequence: the lane
-// offset advances by one sub-chunk per tick, and loads past the sequence end
-// return zeros (the padding tokens), so nothing is masked and no 64-bit
-// address is formed per tick. Used when every offset fits 31 bits.
-struct BufLoad {
-  __amdgpu_buffer_rsrc_t r, w, k, v, a, b;
-  uint32_t loff, step;
-  // kChan / 2 packed pairs of one input: an 8- or 4-byte load
-  template <int N>
-  __device__ __forceinline__ static void one(uint32_t (&dst)[N], __amdgpu_buffer_rsrc_t rs,
-                                             int off) {
-    if constexpr (N == 2) {
-      const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
-      dst[0] = x[0];
-      dst[1] = x[1];
-    } else {
-      dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-    }
-  }
-  __device__ __forceinline__ void operator()(SubIn& d, int64_t j) const {
-    const int off = static_cast<int>(loff + static_cast<uint32_t>(j) * step);
-    one(d.r, r, off);
-    one(d.w, w, off);
-    one(d.k, k, off);
-    one(d.v, v, off);
-    one(d.a, a, off);
-    one(d.b, b, off);
-  }
-};
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const uint16_t* x, const SeqGeom& g,
                                                          bool empty = false) {
   const uint16_t* base = x + g.t_beg * g.tstride + g.hoff;
@@ -547,7 +551,100 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const uint16_t* x, co
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-// The operand waves' pipeline: three fill ticks, then one tick per sub-chunk.
+// Buffer-path input loads: whole 128-byte rows straight into LDS. Each input
+// has one buffer resource per workgroup, based at the sequence's first token
+// and sized to the sequence, so the per-tick offset is a 32-bit add and rows
+// past the sequence end arrive as zeros (the padding tokens; with k = v = 0
+// runs the k and v resources have an empty range). A sub-chunk is 12 loads of
+// 8 tokens x 128 B (6 inputs x 2 halves), three per operand wave: lane l
+// fetches token 8 half + l / 8, 16-byte chunk (l % 8) ^ (token % 8) of the
+// row, so the chunks sit XOR-swizzled by the token (conflict-free reads in
+// read_inputs). One request per 128-byte line instead of four 32-byte pieces.
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                               uint32_t soff, uint32_t lds_base) {
+  // 16 bytes per lane into LDS at lds_base + 16 lane (M0)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               : : "{m0}"(lds_base), "v"(voff), "s"(rs), "s"(soff) : "memory");
+}
+
+struct RowSrc {
+  __amdgpu_buffer_rsrc_t rs[3];  // the input of each of this wave's loads
+  uint32_t voff[3];              // this lane's byte offset of each load at sub-chunk 0
+  uint32_t dst[3];               // byte offset of each load inside a staging slot
+  uint32_t step;                 // bytes per sub-chunk
+};
+
+__device__ __forceinline__ RowSrc row_sources(const Inputs& in, const SeqGeom& g, int lane,
+                                              int part, bool kvz) {
+  RowSrc d;
+  const int c = (lane & 7) ^ (lane >> 3);
+  part = __builtin_amdgcn_readfirstlane(part);  // wave-uniform: the descriptors live in SGPRs
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int gi = 3 * part + i, input = gi >> 1, half = gi & 1;
+    const uint16_t* p = input == 0 ? in.r : input == 1 ? in.w : input == 2 ? in.k
+                      : input == 3 ? in.v : input == 4 ? in.a : in.b;
+    d.rs[i] = seq_rsrc(p, g, kvz && (input == 2 || input == 3));
+    d.voff[i] = 2u * (uint32_t(8 * half + (lane >> 3)) * uint32_t(g.tstride) + uint32_t(8 * c));
+    d.dst[i] = uint32_t((input * kSub + 8 * half) * 128);
+  }
+  d.step = 2u * uint32_t(kSub) * uint32_t(g.tstride);
+  return d;
+}
+
+__device__ __forceinline__ void issue_rows(Shared& sm, const RowSrc& src, int64_t j, int slot) {
+  const uint32_t base = lds_addr(&sm.inb[slot][0][0][0]);
+  const uint32_t soff = uint32_t(j) * src.step;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) buf_load_lds16(src.rs[i], src.voff[i], soff, base + src.dst[i]);
+}
+
+// A tick of the row-loading operand waves ends once this wave's loads of the
+// next sub-chunk have landed (only the three just issued may be in flight),
+// so after the barrier every wave can read all of that sub-chunk's rows.
+__device__ __forceinline__ void rows_tick_end() {
+  wait_vm<3>();
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The row-loading operand pipeline: four fill ticks, then one tick per
+// sub-chunk. Rows of sub-chunk j go to staging slot j % 3 two ticks before
+// their operands are staged.
+__device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, const SeqGeom& g,
+                                                  int64_t n_sub, int lane, int part, float scale,
+                                                  bool kvz) {
+  SubIn d;
+  const RowSrc src = row_sources(in, g, lane, part, kvz);
+  issue_rows(sm, src, 0, 0);
+  issue_rows(sm, src, 1, 1);
+  rows_tick_end();
+  read_inputs(sm, d, 0, lane, part);
+  stage_operands<false>(sm, d, 0, g, lane, part, scale);
+  issue_rows(sm, src, 2, 2);
+  rows_tick_end();
+  read_inputs(sm, d, 1, lane, part);
+  stage_operands<false>(sm, d, 1, g, lane, part, scale);
+  issue_rows(sm, src, 3, 0);
+  rows_tick_end();
+  read_inputs(sm, d, 2, lane, part);
+  stage_operands<false>(sm, d, 2, g, lane, part, scale);
+  issue_rows(sm, src, 4, 1);
+  rows_tick_end();
+  int rs = 0, is = 2;  // staging slots of sub-chunks k+3 and k+5
+  for (int64_t k = 0; k < n_sub; ++k) {
+    read_inputs(sm, d, rs, lane, part);
+    stage_operands<false>(sm, d, k + 3, g, lane, part, scale);
+    issue_rows(sm, src, k + 5, is);
+    rows_tick_end();
+    rs = rs == 2 ? 0 : rs + 1;
+    is = is == 2 ? 0 : is + 1;
+  }
+  wait_vm<0>();  // no load may land in LDS after the workgroup ends
+}
+
+// The register-loading operand pipeline (64-bit input offsets): three fill
+// ticks, then one tick per sub-chunk.
 // Two ticks per iteration so each input buffer keeps its registers (sub-chunk
 // k+3 of tick k is in p1 for even k, p0 for odd k). The loop has a single back
 // edge, after the p0 refill: the compiler's memory-wait placement then knows
@@ -652,6 +749,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
                              : from_zero ? 0.f : hbase[j * kHead + col0 + li];
       }
     if (n_sub > 0) {
+      if constexpr (kBuf) end_tick();  // the row loads' fourth fill tick
       end_tick();  // fill ticks
       end_tick();
       end_tick();
@@ -670,6 +768,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     // ---- T of the next sub-chunk ----
     if (n_sub > 0) {
       const int part = wave - 8 - kOpWaves;
+      if constexpr (kBuf) end_tick();
       end_tick();
       end_tick();
       stage_inverse(sm, 0, lane, part);
@@ -683,6 +782,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     if (n_sub > 0) {
       const int part = wave - 4 - kOpWaves;
       void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
+      if constexpr (kBuf) end_tick();
       end_tick();
       stage_scores(sm, 0, lane, part);
       end_tick();
@@ -699,13 +799,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     // ---- operands ahead of the chain ----
     const int part = wave - 4;
     if constexpr (kBuf) {
-      const bool kvz = fl & WKV7_RUN_KV_ZERO;
-      const BufLoad ld{seq_rsrc(in.r, g), seq_rsrc(in.w, g), seq_rsrc(in.k, g, kvz),
-                       seq_rsrc(in.v, g, kvz), seq_rsrc(in.a, g), seq_rsrc(in.b, g),
-                       2u * (uint32_t(lane & 15) * uint32_t(g.tstride) +
-                             uint32_t(kChan * (4 * part + (lane >> 4)))),
-                       2u * uint32_t(kSub) * uint32_t(g.tstride)};
-      operand_loop<false>(sm, ld, g, n_sub, lane, part, scale);
+      operand_loop_rows(sm, in, g, n_sub, lane, part, scale, fl & WKV7_RUN_KV_ZERO);
     } else {
       const bool kvz = fl & WKV7_RUN_KV_ZERO;
       const auto ld = [&](SubIn& d, int64_t j) {
