@@ -273,8 +273,9 @@ __device__ __forceinline__ void read_inputs(const Shared& sm, SubIn& d, int slot
 
 // Operands of sub-chunk j for key channels [4 kChan part, 4 kChan (part + 1)).
 // kMask: padding tokens arrive as copies of the last real token and are zeroed
-// here; without it the loader has already delivered them as zeros.
-template <bool kMask>
+// here; without it the loader has already delivered them as zeros. kScaled:
+// scale != 1 (fla's default is 1, where R^ = r e^G needs no multiply by it).
+template <bool kMask, bool kScaled>
 __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int64_t j,
                                                const SeqGeom& g, int lane, int part, float scale) {
   constexpr int P = kChan / 2;
@@ -300,7 +301,7 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
     const float ex = row_prev(eh[m], 1.f);                 // decay through token t-1
     const float ie = __builtin_amdgcn_exp2f(-G);
     A_[m] = elem(av, m) * ex;
-    R_[m] = elem(raw.r, m) * scale * eh[m];
+    R_[m] = kScaled ? elem(raw.r, m) * scale * eh[m] : elem(raw.r, m) * eh[m];
     B_[m] = elem(bv, m) * ie;
     K_[m] = elem(kv, m) * ie;
   }
@@ -534,10 +535,10 @@ __device__ __forceinline__ void end_tick() {
 
 // One tick of an operand wave: operands of sub-chunk k+3 (from `cur`, which
 // is then refilled with k+5).
-template <bool kMask, class Load>
+template <bool kMask, bool kScaled, class Load>
 __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Load& load,
                                           const SeqGeom& g, int lane, int part, float scale) {
-  stage_operands<kMask>(sm, cur, k + 3, g, lane, part, scale);
+  stage_operands<kMask, kScaled>(sm, cur, k + 3, g, lane, part, scale);
   load(cur, k + 5);
   end_tick();
 }
@@ -611,6 +612,7 @@ __device__ __forceinline__ void rows_tick_end() {
 // The row-loading operand pipeline: four fill ticks, then one tick per
 // sub-chunk. Rows of sub-chunk j go to staging slot j % 3 two ticks before
 // their operands are staged.
+template <bool kScaled>
 __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, const SeqGeom& g,
                                                   int64_t n_sub, int lane, int part, float scale,
                                                   bool kvz) {
@@ -620,21 +622,21 @@ __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, 
   issue_rows(sm, src, 1, 1);
   rows_tick_end();
   read_inputs(sm, d, 0, lane, part);
-  stage_operands<false>(sm, d, 0, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, d, 0, g, lane, part, scale);
   issue_rows(sm, src, 2, 2);
   rows_tick_end();
   read_inputs(sm, d, 1, lane, part);
-  stage_operands<false>(sm, d, 1, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, d, 1, g, lane, part, scale);
   issue_rows(sm, src, 3, 0);
   rows_tick_end();
   read_inputs(sm, d, 2, lane, part);
-  stage_operands<false>(sm, d, 2, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, d, 2, g, lane, part, scale);
   issue_rows(sm, src, 4, 1);
   rows_tick_end();
   int rs = 0, is = 2;  // staging slots of sub-chunks k+3 and k+5
   for (int64_t k = 0; k < n_sub; ++k) {
     read_inputs(sm, d, rs, lane, part);
-    stage_operands<false>(sm, d, k + 3, g, lane, part, scale);
+    stage_operands<false, kScaled>(sm, d, k + 3, g, lane, part, scale);
     issue_rows(sm, src, k + 5, is);
     rows_tick_end();
     rs = rs == 2 ? 0 : rs + 1;
@@ -649,7 +651,7 @@ __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, 
 // k+3 of tick k is in p1 for even k, p0 for odd k). The loop has a single back
 // edge, after the p0 refill: the compiler's memory-wait placement then knows
 // that p0's loads are younger than p1's and waits for p1 alone.
-template <bool kMask, class Load>
+template <bool kMask, bool kScaled, class Load>
 __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const SeqGeom& g,
                                              int64_t n_sub, int lane, int part, float scale) {
   SubIn p0, p1;
@@ -657,21 +659,21 @@ __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const S
   ld(p1, 1);
   // fill ticks -3 .. -1 (stages of sub-chunks past the end, if any, work on
   // zero tokens and are never consumed)
-  stage_operands<kMask>(sm, p0, 0, g, lane, part, scale);
+  stage_operands<kMask, kScaled>(sm, p0, 0, g, lane, part, scale);
   ld(p0, 2);
   __syncthreads();
-  stage_operands<kMask>(sm, p1, 1, g, lane, part, scale);
+  stage_operands<kMask, kScaled>(sm, p1, 1, g, lane, part, scale);
   ld(p1, 3);
   __syncthreads();
-  stage_operands<kMask>(sm, p0, 2, g, lane, part, scale);
+  stage_operands<kMask, kScaled>(sm, p0, 2, g, lane, part, scale);
   ld(p0, 4);
   __syncthreads();
   int64_t k = 0;
   for (; k + 1 < n_sub; k += 2) {
-    prep_tick<kMask>(sm, p1, k, ld, g, lane, part, scale);
-    prep_tick<kMask>(sm, p0, k + 1, ld, g, lane, part, scale);
+    prep_tick<kMask, kScaled>(sm, p1, k, ld, g, lane, part, scale);
+    prep_tick<kMask, kScaled>(sm, p0, k + 1, ld, g, lane, part, scale);
   }
-  if (k < n_sub) prep_tick<kMask>(sm, p1, k, ld, g, lane, part, scale);
+  if (k < n_sub) prep_tick<kMask, kScaled>(sm, p1, k, ld, g, lane, part, scale);
 }
 
 // Sixteen wavefronts in four kinds: waves 0-3 run the state chain (wave q
@@ -697,7 +699,7 @@ struct Runs {
   void* y_alt;            // like y
 };
 
-template <bool kF32Out, bool kBuf>
+template <bool kF32Out, bool kBuf, bool kScaled>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ seq_order, int nseq,
@@ -799,7 +801,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
     // ---- operands ahead of the chain ----
     const int part = wave - 4;
     if constexpr (kBuf) {
-      operand_loop_rows(sm, in, g, n_sub, lane, part, scale, fl & WKV7_RUN_KV_ZERO);
+      operand_loop_rows<kScaled>(sm, in, g, n_sub, lane, part, scale, fl & WKV7_RUN_KV_ZERO);
     } else {
       const bool kvz = fl & WKV7_RUN_KV_ZERO;
       const auto ld = [&](SubIn& d, int64_t j) {
@@ -809,7 +811,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
           for (int i = 0; i < kChan / 2; ++i) d.k[i] = d.v[i] = 0u;
         }
       };
-      operand_loop<true>(sm, ld, g, n_sub, lane, part, scale);
+      operand_loop<true, kScaled>(sm, ld, g, n_sub, lane, part, scale);
     }
   }
 }
@@ -830,11 +832,17 @@ int prefill_launch(float* wkv_layer, int64_t num_rows, int32_t H, const int32_t*
   // Buffer-resource input loads need every byte offset of a sequence (plus the
   // look-ahead past its end) to fit 31 bits.
   const bool buf = (total_tokens + 6 * kSub) * int64_t(H) * kHead * 2 < (int64_t(1) << 31);
-  auto launch = [&](auto f32, auto bufc) {
-    prefill_chunked_kernel<decltype(f32)::value, decltype(bufc)::value>
+  auto launch3 = [&](auto f32, auto bufc, auto sc) {
+    prefill_chunked_kernel<decltype(f32)::value, decltype(bufc)::value, decltype(sc)::value>
         <<<unsigned(blocks), kThreads, 0, s>>>(wkv_layer, num_rows, H, slot_ids, cu_seqlens,
                                                seq_order, nseq, in, y, total_tokens, zero_init,
                                                scale, runs);
+  };
+  auto launch = [&](auto f32, auto bufc) {
+    if (scale != 1.0f)
+      launch3(f32, bufc, std::true_type{});
+    else
+      launch3(f32, bufc, std::false_type{});
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
