@@ -26,7 +26,8 @@
 //                              also store sub-chunk k-1's y from the staging
 //                              buffer as whole rows
 //   operands  (sub-chunk k+3): decays and operand matrices, 16 key channels
-//                              per wave
+//                              per wave (in the buffer path the cumulative
+//                              sums G are one MFMA with a triangle of ones)
 // Sub-chunk j lives in ring slot j % 4 from tick j-3 to tick j; its inputs
 // are loaded two ticks before they are used, as whole 128-byte rows straight
 // into an LDS staging ring of three sub-chunks (the buffer path, every batch
@@ -249,9 +250,10 @@ __device__ __forceinline__ void st_pairs(uint16_t* p, const uint32_t (&x)[N]) {
     *reinterpret_cast<uint32_t*>(p) = x[0];
 }
 
-// This lane's kChan channels of token t = lane % 16 of every input, from
-// staging slot `slot` (rows stored with their 16-byte chunks XOR-swizzled by
-// the token, see row_sources).
+// This lane's kChan channels of token t = lane % 16 of every input but w, and
+// w transposed (channel 16 part + t at tokens 4 cg .. 4 cg + 3), from staging
+// slot `slot` (rows stored with their 16-byte chunks XOR-swizzled by the
+// token, see row_sources).
 __device__ __forceinline__ void read_inputs(const Shared& sm, SubIn& d, int slot, int lane,
                                             int part) {
   const int t = lane & 15, cg = lane >> 4;
@@ -264,7 +266,17 @@ __device__ __forceinline__ void read_inputs(const Shared& sm, SubIn& d, int slot
     x[1] = v.y;
   };
   rd(d.r, 0);
-  rd(d.w, 1);
+  {
+    // w transposed for the prefix-sum product of stage_operands: this lane
+    // reads token 4 cg + t / 4 at channels 16 part + 4 (t % 4) and receives
+    // channel 16 part + t at tokens 4 cg .. 4 cg + 3
+    const int ts = 4 * cg + (t >> 2), ch = 16 * part + 4 * (t & 3);
+    const int wpos = (((ch >> 3) ^ (ts & 7)) * 16) + (ch & 7) * 2;
+    const uint2 v = ld_tr(reinterpret_cast<const uint16_t*>(
+        reinterpret_cast<const unsigned char*>(&sm.inb[slot][1][ts][0]) + wpos));
+    d.w[0] = v.x;
+    d.w[1] = v.y;
+  }
   rd(d.k, 2);
   rd(d.v, 3);
   rd(d.a, 4);
@@ -272,16 +284,19 @@ __device__ __forceinline__ void read_inputs(const Shared& sm, SubIn& d, int slot
 }
 
 // Operands of sub-chunk j for key channels [4 kChan part, 4 kChan (part + 1)).
-// kMask: padding tokens arrive as copies of the last real token and are zeroed
-// here; without it the loader has already delivered them as zeros. kScaled:
-// scale != 1 (fla's default is 1, where R^ = r e^G needs no multiply by it).
-template <bool kMask, bool kScaled>
+// kRows: the inputs come from the row-staging ring (read_inputs), where padding
+// tokens are zeros already (the row loads stop at the sequence end) and w
+// arrives transposed for the prefix-sum product; otherwise (registers, in
+// operand layout) padding tokens arrive as copies of the last real token and
+// are zeroed here. kScaled: scale != 1 (fla's default is 1, where R^ = r e^G
+// needs no multiply by it).
+template <bool kRows, bool kScaled>
 __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int64_t j,
                                                const SeqGeom& g, int lane, int part, float scale) {
   constexpr int P = kChan / 2;
   Slot& S = sm.slot[j & (kRing - 1)];
   const int t = lane & 15, cg = lane >> 4;
-  const bool valid = !kMask || g.t_beg + kSub * j + t < g.t_end;
+  const bool valid = kRows || g.t_beg + kSub * j + t < g.t_end;
   // r and v of padding tokens only meet zero rows and columns (their k, b
   // and a are zero, and their y is not stored), so they need no masking.
   uint32_t wv[P], kv[P], av[P], bv[P];
@@ -294,9 +309,25 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
   }
   constexpr float kLog2e = 1.4426950408889634f;
   float A_[kChan], R_[kChan], B_[kChan], K_[kChan], eh[kChan];
+  f32x4 wsum = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kRows) {
+    // wsum[m] = sum_{s <= t} w[s][c_m] for this lane's token t and channels
+    // c_m, as the product (W^T L^T)[c][t]: A = W^T (wv holds channel 16 part + t
+    // at tokens 4 cg .. 4 cg + 3) and the constant B[s][t] = [s <= t]. The
+    // matrix cores take the sum off the vector ALUs, which the four wave
+    // kinds share.
+    const int s0 = 4 * cg;
+    const uint32_t one = 0x3f80u;  // bf16 1.0
+    const uint2 lt = make_uint2((s0 <= t ? one : 0u) | (s0 + 1 <= t ? one << 16 : 0u),
+                                (s0 + 2 <= t ? one : 0u) | (s0 + 3 <= t ? one << 16 : 0u));
+    wsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+        __builtin_bit_cast(s16x4, make_uint2(wv[0], wv[1])), __builtin_bit_cast(s16x4, lt),
+        wsum, 0, 0, 0);
+  }
 #pragma unroll
   for (int m = 0; m < kChan; ++m) {
-    const float G = row_prefix_sum(elem(wv, m) * kLog2e);  // log2 decay through token t
+    // log2 decay through token t
+    const float G = kRows ? wsum[m] * kLog2e : row_prefix_sum(elem(wv, m) * kLog2e);
     eh[m] = __builtin_amdgcn_exp2f(G);
     const float ex = row_prev(eh[m], 1.f);                 // decay through token t-1
     const float ie = __builtin_amdgcn_exp2f(-G);
@@ -535,10 +566,10 @@ __device__ __forceinline__ void end_tick() {
 
 // One tick of an operand wave: operands of sub-chunk k+3 (from `cur`, which
 // is then refilled with k+5).
-template <bool kMask, bool kScaled, class Load>
+template <bool kScaled, class Load>
 __device__ __forceinline__ void prep_tick(Shared& sm, SubIn& cur, int64_t k, const Load& load,
                                           const SeqGeom& g, int lane, int part, float scale) {
-  stage_operands<kMask, kScaled>(sm, cur, k + 3, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, cur, k + 3, g, lane, part, scale);
   load(cur, k + 5);
   end_tick();
 }
@@ -622,21 +653,21 @@ __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, 
   issue_rows(sm, src, 1, 1);
   rows_tick_end();
   read_inputs(sm, d, 0, lane, part);
-  stage_operands<false, kScaled>(sm, d, 0, g, lane, part, scale);
+  stage_operands<true, kScaled>(sm, d, 0, g, lane, part, scale);
   issue_rows(sm, src, 2, 2);
   rows_tick_end();
   read_inputs(sm, d, 1, lane, part);
-  stage_operands<false, kScaled>(sm, d, 1, g, lane, part, scale);
+  stage_operands<true, kScaled>(sm, d, 1, g, lane, part, scale);
   issue_rows(sm, src, 3, 0);
   rows_tick_end();
   read_inputs(sm, d, 2, lane, part);
-  stage_operands<false, kScaled>(sm, d, 2, g, lane, part, scale);
+  stage_operands<true, kScaled>(sm, d, 2, g, lane, part, scale);
   issue_rows(sm, src, 4, 1);
   rows_tick_end();
   int rs = 0, is = 2;  // staging slots of sub-chunks k+3 and k+5
   for (int64_t k = 0; k < n_sub; ++k) {
     read_inputs(sm, d, rs, lane, part);
-    stage_operands<false, kScaled>(sm, d, k + 3, g, lane, part, scale);
+    stage_operands<true, kScaled>(sm, d, k + 3, g, lane, part, scale);
     issue_rows(sm, src, k + 5, is);
     rows_tick_end();
     rs = rs == 2 ? 0 : rs + 1;
@@ -651,7 +682,7 @@ __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, 
 // k+3 of tick k is in p1 for even k, p0 for odd k). The loop has a single back
 // edge, after the p0 refill: the compiler's memory-wait placement then knows
 // that p0's loads are younger than p1's and waits for p1 alone.
-template <bool kMask, bool kScaled, class Load>
+template <bool kScaled, class Load>
 __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const SeqGeom& g,
                                              int64_t n_sub, int lane, int part, float scale) {
   SubIn p0, p1;
@@ -659,21 +690,21 @@ __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const S
   ld(p1, 1);
   // fill ticks -3 .. -1 (stages of sub-chunks past the end, if any, work on
   // zero tokens and are never consumed)
-  stage_operands<kMask, kScaled>(sm, p0, 0, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, p0, 0, g, lane, part, scale);
   ld(p0, 2);
   __syncthreads();
-  stage_operands<kMask, kScaled>(sm, p1, 1, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, p1, 1, g, lane, part, scale);
   ld(p1, 3);
   __syncthreads();
-  stage_operands<kMask, kScaled>(sm, p0, 2, g, lane, part, scale);
+  stage_operands<false, kScaled>(sm, p0, 2, g, lane, part, scale);
   ld(p0, 4);
   __syncthreads();
   int64_t k = 0;
   for (; k + 1 < n_sub; k += 2) {
-    prep_tick<kMask, kScaled>(sm, p1, k, ld, g, lane, part, scale);
-    prep_tick<kMask, kScaled>(sm, p0, k + 1, ld, g, lane, part, scale);
+    prep_tick<kScaled>(sm, p1, k, ld, g, lane, part, scale);
+    prep_tick<kScaled>(sm, p0, k + 1, ld, g, lane, part, scale);
   }
-  if (k < n_sub) prep_tick<kMask, kScaled>(sm, p1, k, ld, g, lane, part, scale);
+  if (k < n_sub) prep_tick<kScaled>(sm, p1, k, ld, g, lane, part, scale);
 }
 
 // Sixteen wavefronts in four kinds: waves 0-3 run the state chain (wave q
@@ -811,7 +842,7 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
           for (int i = 0; i < kChan / 2; ++i) d.k[i] = d.v[i] = 0u;
         }
       };
-      operand_loop<true, kScaled>(sm, ld, g, n_sub, lane, part, scale);
+      operand_loop<kScaled>(sm, ld, g, n_sub, lane, part, scale);
     }
   }
 }
