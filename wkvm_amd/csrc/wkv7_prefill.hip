@@ -67,6 +67,8 @@ constexpr int kRing = 4;
 constexpr int kOpWaves = 4;                      // operand wavefronts
 constexpr int kChan = kHead / (4 * kOpWaves);  // key channels per operand lane
 constexpr int kThreads = kWave * (12 + kOpWaves);  // 4 state + operand + 4 score + 4 inverse
+// The row-staging reads and the decay-sum product take 4 channels per lane (one 8-byte piece).
+static_assert(kChan == 4, "operand lanes hold 4 key channels");
 // LDS layouts. Every operand array is [token][64 channels] with unpadded
 // 128 B rows whose 16 B chunks are XOR-swizzled by the row (chunk c of row r
 // sits at c ^ (r & 7)): the MFMA operand loads (16 rows x 4 chunks per
