@@ -666,15 +666,27 @@ __device__ __forceinline__ void operand_loop_rows(Shared& sm, const Inputs& in, 
   stage_operands<true, kScaled>(sm, d, 2, g, lane, part, scale);
   issue_rows(sm, src, 4, 1);
   rows_tick_end();
-  int rs = 0, is = 2;  // staging slots of sub-chunks k+3 and k+5
-  for (int64_t k = 0; k < n_sub; ++k) {
-    read_inputs(sm, d, rs, lane, part);
+  // Sub-chunk k+3 is read from staging slot k % 3 and k+5 goes to slot
+  // (k + 2) % 3. The loop is unrolled by three so that both slots are
+  // constants in each body: the operand waves are the longest role of the
+  // tick, and the slot arithmetic was scalar work on their path.
+  auto tick = [&](int64_t k, auto rs, auto is) {
+    read_inputs(sm, d, decltype(rs)::value, lane, part);
     stage_operands<true, kScaled>(sm, d, k + 3, g, lane, part, scale);
-    issue_rows(sm, src, k + 5, is);
+    issue_rows(sm, src, k + 5, decltype(is)::value);
     rows_tick_end();
-    rs = rs == 2 ? 0 : rs + 1;
-    is = is == 2 ? 0 : is + 1;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  int64_t k = 0;
+  for (; k + 3 <= n_sub; k += 3) {
+    tick(k, S0{}, S2{});
+    tick(k + 1, S1{}, S0{});
+    tick(k + 2, S2{}, S1{});
   }
+  if (k < n_sub) tick(k++, S0{}, S2{});
+  if (k < n_sub) tick(k++, S1{}, S0{});
   wait_vm<0>();  // no load may land in LDS after the workgroup ends
 }
 
