@@ -117,6 +117,33 @@ def test_cfg2_full_size_zero_init(dev):
     assert bool((gpool[others] == 7.0).all())
 
 
+def test_repeated_runs_are_bit_identical(dev):
+    """The same ragged batch (slot state in, fp32 y) run six times gives
+    bit-identical y and final states every time: no result may depend on
+    timing (matrix-core results read back by vector instructions before they
+    are ready, LDS reads racing a tick's writes)."""
+    H, S = 32, 16
+    lens = [4096, 4001, 17, 1, 100, 2000, 33, 3000]
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    gen = synthetic.make_generator(5)
+    vecs = synthetic.wkv7_vectors((cu[-1], H, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    pool0 = torch.zeros((S + 1, H, 64, 64))
+    pool0[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    pool0 = pool0.to(dev)
+    ids = list(range(1, len(lens) + 1))
+    ref = None
+    for rep in range(6):
+        pool = pool0.clone()
+        y = ops.wkv7_prefill_varlen(pool, ids, cu, *xs, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        if ref is None:
+            ref = (y, pool)
+        else:
+            assert torch.equal(y, ref[0]), f"run {rep}: y differs"
+            assert torch.equal(pool, ref[1]), f"run {rep}: final states differ"
+
+
 def test_chunk_split_invariance_through_the_slot(dev):
     """CF6: one call over T tokens equals the runner's chunked re-entry through
     the slot (prefill_chunk 64, 100 and 4096), as a preempted request's would.

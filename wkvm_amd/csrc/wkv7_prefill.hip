@@ -319,12 +319,13 @@ __device__ __forceinline__ void stage_operands(Shared& sm, const SubIn& raw, int
     // matrix cores take the sum off the vector ALUs, which the four wave
     // kinds share.
     const int s0 = 4 * cg;
+    // On the 16x16x32 instruction with zero upper halves: results of the legacy
+    // 16x16x16 one, read back by VALU, have come out wrong now and then on
+    // gfx950 with this toolchain's wait-state insertion.
     const uint32_t one = 0x3f80u;  // bf16 1.0
-    const uint2 lt = make_uint2((s0 <= t ? one : 0u) | (s0 + 1 <= t ? one << 16 : 0u),
-                                (s0 + 2 <= t ? one : 0u) | (s0 + 3 <= t ? one << 16 : 0u));
-    wsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-        __builtin_bit_cast(s16x4, make_uint2(wv[0], wv[1])), __builtin_bit_cast(s16x4, lt),
-        wsum, 0, 0, 0);
+    const uint4 lt = make_uint4((s0 <= t ? one : 0u) | (s0 + 1 <= t ? one << 16 : 0u),
+                                (s0 + 2 <= t ? one : 0u) | (s0 + 3 <= t ? one << 16 : 0u), 0u, 0u);
+    wsum = mma32(make_uint4(wv[0], wv[1], 0u, 0u), lt, wsum);
   }
 #pragma unroll
   for (int m = 0; m < kChan; ++m) {
