@@ -5,10 +5,10 @@
 // contiguous bytes. Work is cut into 16 KiB tiles of one row; each of a block's
 // 512 threads moves 2 vectors of the widest type the pointers, strides and row
 // size allow. Pure HBM streaming: no LDS, loads of one tile are all issued
-// before its stores, and both carry non-temporal hints (5 % faster on a 7B fork
-// round than plain accesses). On that round 512 x 2 runs 3 % faster than
-// 256 x 4; deeper unrolling, 768- or 1024-thread blocks and a persistent grid
-// are all slower.
+// before its stores, and both carry non-temporal hints (5 % faster than plain
+// accesses when forking 128 slots of the 7B shape). On that fork 512 x 2 runs
+// 3 % faster than 256 x 4; deeper unrolling, 768- or 1024-thread blocks and a
+// persistent grid are all slower.
 #include "wkv7_common.h"
 
 namespace wkv7 {
