@@ -5,7 +5,8 @@ are covered by test_gpu_store.py.
 
 Pinned against the reference's behaviour (wkvm/store.py): the fingerprint is
 the sha256 of the same key string; handles are ``name@version``; COLD files
-are ``<name>_v<version>.safetensors`` holding tensors "wkv" and "shift"; the
+are the handle with '@' replaced by '_v' plus ``.safetensors``, holding
+tensors "wkv" and "shift"; the
 index maps handles to record fields plus a ``cold`` flag; ``decay`` is an
 fp32 multiply of wkv only; ``merge`` is (1 - w) a + w b in fp32 with one
 rounding per operation, cast back to each family's dtype."""
@@ -181,3 +182,33 @@ def test_save_host_validation_warm_view_and_shared_forks(tmp_path):
     st.delete(h)  # the fork keeps the shared tensors
     assert torch.equal(st.host_tensors(kid)["wkv"], t["wkv"])
     assert not (tmp_path / "p_v0.safetensors").exists()
+
+
+def test_cold_file_name_of_a_name_with_at_sign(tmp_path):
+    """The COLD file name is the handle with every '@' replaced by '_v'
+    (wkvm/store.py:257-258), so a name that holds '@' maps to the file the
+    reference writes: 'u@h' version 1 -> 'u_vh_v1.safetensors'. A directory
+    laid out that way (index + file, written here by hand) opens and loads."""
+    bank = _bank()
+    st = StateStore(bank, tmp_path)
+    t = _tensors(bank, 9)
+    st.save_host("u@h", t, 2, [4, 5, 6])
+    h = _put(st, "u@h", t)
+    assert h == "u@h@1"
+    path = st.persist(h)
+    assert path.name == "u_vh_v1.safetensors" and path.exists()
+    assert not list(tmp_path.glob("*.partial"))  # the temporary name was renamed away
+    st.delete(h)
+    assert not path.exists()
+
+    ref_dir = tmp_path / "ref"
+    ref_dir.mkdir()
+    from safetensors.torch import save_file
+    save_file({k: v.contiguous() for k, v in t.items()}, str(ref_dir / "u_vh_v0.safetensors"))
+    row = {"name": "u@h", "version": 0, "fingerprint": st.fingerprint,
+           "num_computed_tokens": 2, "token_ids": [4, 5, 6], "parent": None, "rule": None,
+           "rule_params": {}, "cold": True}
+    (ref_dir / "index.json").write_text(json.dumps({"u@h@0": row}))
+    st2 = StateStore(bank, ref_dir)
+    got = st2.host_tensors("u@h@0")
+    assert torch.equal(got["wkv"], t["wkv"]) and torch.equal(got["shift"], t["shift"])

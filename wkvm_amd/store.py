@@ -26,8 +26,10 @@ reference has it (wkvm/store.py:39-57, 80-84, 228-256):
   1 + the highest live version (0 for a new name);
 * the index file ``index.json``: handle -> record fields (``token_ids`` as a
   list) plus a boolean ``cold``;
-* COLD files ``<name>_v<version>.safetensors`` holding tensors ``wkv`` and
-  ``shift``;
+* COLD files named by the handle with every ``@`` replaced by ``_v``
+  (``<name>_v<version>.safetensors`` for a name without ``@``), holding
+  tensors ``wkv`` and ``shift``; the file is fsync'd and renamed into place
+  before the index marks the record ``cold``;
 * the model fingerprint: the first 16 hex digits of the sha256 of
   ``rwkv7:L{n_layer}:wkv{wkv_shape}:shift{shift_shape}:{dtype}``;
 * the two built-in rules: ``decay`` scales ``wkv`` by ``alpha`` (default
@@ -129,11 +131,7 @@ class _Catalog:
             f.flush()
             os.fsync(f.fileno())
         os.replace(self._partial, self.path)
-        fd = os.open(self.path.parent, os.O_RDONLY)
-        try:
-            os.fsync(fd)
-        finally:
-            os.close(fd)
+        _fsync_dir(self.path.parent)
 
     def entries(self) -> list[_Entry]:
         """Records of the last complete index; their WARM tensors died with
@@ -334,8 +332,10 @@ class StateStore:
     # -- WARM <-> COLD ------------------------------------------------------------
 
     def _cold_path(self, handle: str) -> Path:
-        record = self.get(handle)
-        return self.store_dir / f"{record.name}_v{record.version}.safetensors"
+        # The reference derives the file name from the handle by replacing
+        # every '@' with '_v' (wkvm/store.py:257-258); a name that itself
+        # holds '@' must map to the same file for a shared store directory.
+        return self.store_dir / f"{self.get(handle).handle.replace('@', '_v')}.safetensors"
 
     def persist(self, handle: str) -> Path:
         """Write the record's COLD file and mark it in the index; a record
@@ -346,7 +346,14 @@ class StateStore:
             from safetensors.torch import save_file
 
             host = self.host_tensors(handle)
-            save_file({fam: host[fam].contiguous() for fam in FAMILIES}, str(path))
+            # The index must never name a file whose bytes are not durable:
+            # write a temporary file, fsync it, rename it into place and fsync
+            # the directory before the index marks the record COLD.
+            partial = path.with_name(path.name + ".partial")
+            save_file({fam: host[fam].contiguous() for fam in FAMILIES}, str(partial))
+            _fsync_file(partial)
+            os.replace(partial, path)
+            _fsync_dir(self.store_dir)
             entry.on_disk = True
             self._catalog.store(self._entries.values())
         return path
@@ -364,8 +371,7 @@ class StateStore:
         if entry is None:
             return
         if entry.on_disk:
-            (self.store_dir / f"{entry.record.name}_v{entry.record.version}.safetensors"
-             ).unlink(missing_ok=True)
+            (self.store_dir / f"{handle.replace('@', '_v')}.safetensors").unlink(missing_ok=True)
         self._catalog.store(self._entries.values())
 
 
@@ -377,6 +383,19 @@ def rule_decay(tensors: dict[str, torch.Tensor], params: dict) -> dict[str, torc
     wkv = tensors["wkv"]
     out["wkv"] = wkv.float().mul(alpha).to(wkv.dtype)
     return out
+
+
+def _fsync_file(path: Path) -> None:
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.fsync(fd)
+    finally:
+        os.close(fd)
+
+
+def _fsync_dir(directory: Path) -> None:
+    # a rename is durable once the directory entry is
+    _fsync_file(directory)
 
 
 def _round_up(n: int, to: int) -> int:
