@@ -23,9 +23,13 @@ with the rounding contract of ``include/wkv7.h`` (fp32 arithmetic, one bf16
 rounding per output; ``delta`` rounded to bf16 as the shift's own output).
 Parity status: ``token_shift_mix`` is bit-exact by construction of that
 contract and pinned by the invariants in tests/test_timemix_oracle.py;
-``time_mix_inputs`` / ``time_mix_output`` are pinned by invariants
-(unit-norm kk, gate limits, GroupNorm moments, zero-parameter limits). Agreement
-with fla's own bf16 intermediate roundings is "parity unpinned".
+``time_mix_inputs`` / ``time_mix_output`` are pinned by invariants and closed
+forms: unit-norm kk, kk of a one-hot and a two-channel ``k_k`` (which fixes
+where ``k_k`` enters), the gate limits, the GroupNorm moments under any
+per-channel ``ln_w`` / ``ln_b`` (which fixes the affine ``n ln_w + ln_b``) and
+the bonus term of a one-hot ``r_k``; the tests also plant a dropped ``k_k``
+and a swapped affine in copies of these functions and see the pins fail.
+Agreement with fla's own bf16 intermediate roundings is "parity unpinned".
 """
 
 from __future__ import annotations

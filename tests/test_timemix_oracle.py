@@ -7,9 +7,11 @@ is the last token's input, so any split of a sequence into chunks threaded
 through the slot row, and a token-by-token decode, equal one pass, bit for
 bit (wkvm/models/rwkv7.py:25-27, wkvm/runner/runner.py:12-14). Exact
 arithmetic cases (small-integer inputs) pin which row is "prev". The other
-stages are pinned by invariants their definitions fix: a unit-norm kk, the
-exact limits of every sigmoid gate, the GroupNorm moments and the bonus term
-of a one-hot r_k."""
+stages are pinned by invariants their definitions fix: a unit-norm kk and
+its closed form under a one-hot or two-channel k_k, the exact limits of every
+sigmoid gate, the GroupNorm moments under a per-channel affine ln_w / ln_b,
+and the bonus term of a one-hot r_k. Copies of the oracle with a planted
+mistake (k_k dropped; n + ln_w ln_b) must fail those pins."""
 
 from __future__ import annotations
 
@@ -143,6 +145,59 @@ def test_inputs_limits():
     assert np.array_equal(TM.time_mix_inputs(H, **a)["v"], a["v"])
 
 
+def _check_kk_one_hot(inputs_fn):
+    """k_k one-hot on channel c of each head: kk = normalize(k * k_k) is
+    sign(k_c) e_c, so a = -sign(k_c) e_c and b = -a sigmoid(a_lora), exactly.
+    An oracle that drops k_k normalises all 64 channels of k instead."""
+    T, H = 5, 3
+    D = H * 64
+    chans = [7, 40, 63]
+    k_k = np.zeros(D)
+    for h, c in enumerate(chans):
+        k_k[64 * h + c] = RNG.uniform(0.5, 2.0)
+    H, a = _inputs(T=T, H=H, k_k=k_k)
+    o = inputs_fn(H, **a)
+    expect_a = np.zeros((T, D))
+    for h, c in enumerate(chans):
+        expect_a[:, 64 * h + c] = -np.sign(a["k"][:, 64 * h + c])
+    assert np.array_equal(o["a"], expect_a)
+    assert np.allclose(o["b"], -expect_a / (1 + np.exp(-a["a_lora"])), rtol=0, atol=1e-15)
+
+
+def _check_kk_two_channels(inputs_fn):
+    """Two live channels per head: kk is (k_c1 k_k[c1], k_c2 k_k[c2]) over its
+    own norm, which a per-channel k_k changes and a dropped k_k does not."""
+    T, H = 4, 2
+    D = H * 64
+    k_k = np.zeros(D)
+    k_k[3], k_k[11] = 0.25, 3.0
+    k_k[64 + 0], k_k[64 + 50] = 2.0, 0.5
+    H, a = _inputs(T=T, H=H, k_k=k_k)
+    o = inputs_fn(H, **a)
+    for c1, c2 in ((3, 11), (64, 114)):
+        x1, x2 = a["k"][:, c1] * k_k[c1], a["k"][:, c2] * k_k[c2]
+        n = np.hypot(x1, x2)
+        assert np.allclose(o["a"][:, c1], -x1 / n, atol=1e-14)
+        assert np.allclose(o["a"][:, c2], -x2 / n, atol=1e-14)
+
+
+def test_inputs_kk_pins():
+    _check_kk_one_hot(TM.time_mix_inputs)
+    _check_kk_two_channels(TM.time_mix_inputs)
+
+
+def _inputs_without_kk(H, k, v, w_lora, a_lora, k_k, k_a, v_lora=None, v_first=None):
+    # planted mistake: k_k ignored in the normalisation
+    return TM.time_mix_inputs(H, k, v, w_lora, a_lora, np.ones_like(k_k), k_a, v_lora, v_first)
+
+
+def test_kk_pins_fail_on_an_oracle_without_kk():
+    with pytest.raises(AssertionError):
+        _check_kk_one_hot(_inputs_without_kk)
+    with pytest.raises(AssertionError):
+        _check_kk_two_channels(_inputs_without_kk)
+
+
 # -- WKV output ------------------------------------------------------------------
 
 def test_output_groupnorm_moments():
@@ -181,6 +236,48 @@ def test_output_bonus_one_hot_and_gate():
     out_g, _ = TM.time_mix_output(H, RNG.standard_normal((T, H, 64)), r, k, v, g, r_k, z, z,
                                   1e-5)
     assert np.allclose(out_g, out * g, atol=1e-12)
+
+
+def _check_ln_affine(output_fn):
+    """GroupNorm affine per channel: out = n ln_w + ln_b (r_k = 0, g = 1), so
+    (out - ln_b) / ln_w has mean 0 and second moment var / (var + eps) per
+    head, for any per-channel ln_w and ln_b. An oracle that forms
+    n + ln_w ln_b, or drops either parameter, breaks one of the two moments."""
+    T, H = 6, 3
+    D = H * 64
+    eps = 1e-3
+    y = RNG.standard_normal((T, H, 64)) * 2 - 0.5
+    ln_w = RNG.uniform(0.5, 2.0, D) * RNG.choice([-1.0, 1.0], D)
+    ln_b = RNG.standard_normal(D)
+    z = np.zeros(D)
+    args = dict(r=RNG.standard_normal((T, D)), k=RNG.standard_normal((T, D)),
+                v=RNG.standard_normal((T, D)), g=np.ones((T, D)), r_k=z, eps=eps)
+    out, _ = output_fn(H, y, ln_w=ln_w, ln_b=ln_b, **args)
+    n = ((out - ln_b) / ln_w).reshape(T, H, 64)
+    var = y.var(axis=-1)
+    assert np.allclose(n.mean(axis=-1), 0, atol=1e-12)
+    assert np.allclose((n ** 2).mean(axis=-1), var / (var + eps), atol=1e-12)
+    # a constant ln_w = lam scales the moments by lam^2 (ln_b = 0)
+    lam = -1.75
+    out, _ = output_fn(H, y, ln_w=np.full(D, lam), ln_b=z, **args)
+    oh = out.reshape(T, H, 64)
+    assert np.allclose((oh ** 2).mean(axis=-1), lam * lam * var / (var + eps), atol=1e-12)
+
+
+def test_output_ln_affine_pins():
+    _check_ln_affine(TM.time_mix_output)
+
+
+def _output_affine_swapped(H, y, r, k, v, g, r_k, ln_w, ln_b, eps):
+    # planted mistake: n + ln_w ln_b in place of n ln_w + ln_b
+    D = H * 64
+    out, scale = TM.time_mix_output(H, y, r, k, v, g, r_k, np.ones(D), ln_w * ln_b, eps)
+    return out, scale
+
+
+def test_ln_affine_pins_fail_on_a_swapped_affine():
+    with pytest.raises(AssertionError):
+        _check_ln_affine(_output_affine_swapped)
 
 
 # -- C ABI argument errors (no launch) -----------------------------------------------
