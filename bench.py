@@ -58,7 +58,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--only", choices=("fla_decode", "fork_decode_7b", "mixed_ragged",
-                                       "decode_graph", "state_store", "time_mix", "proj"),
+                                       "decode_graph", "state_store", "time_mix", "proj",
+                                       "request_prefill"),
                     help="run just this extra section and print its result as JSON (for "
                          "rocprofv3 runs; not the benchmark line)")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -425,6 +426,86 @@ def bench_prefill_one_sequence(torch, dev, args):
     log(f"prefill one sequence of {T} tokens (H={H}): one pass {one:.3f} ms, "
         f"4 segments {seg:.3f} ms")
     del xs, pool, y
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_request_prefill(torch, dev, args, launcher):
+    """One 4,096-token request at the reference's own call pattern: RWKV7Runner
+    prefill in prefill_chunk = 512 slices at batch 1 (wkvm/runner/runner.py:
+    52-61, one request per call from wkvm/engine.py:152-153), each slice
+    through every one of the 24 layers (1.5B heads, each layer its own
+    state). Three ways in, each from the same zero-initialised state:
+    * fla: chunk_rwkv7(initial_state=, output_final_state=True) per layer and
+      slice, as the model layer calls it (wkvm/models/rwkv7.py:108-113);
+    * runner: WKV7Runner.prefill on the slot pool (state in its slot row);
+    * launcher: the same 192 launches through pre-bound ctypes calls, i.e. the
+      kernels with no per-call Python work (what the GPU side takes).
+    Whole-request time from events around it (inputs resident in HBM)."""
+    from wkvm_amd import ops, synthetic
+    from wkvm_amd.layout import RWKV7StateLayout
+    from wkvm_amd.runner import WKV7Runner
+    from wkvm_amd.state import RWKV7StateBank
+
+    H, T, L, chunk = 32, 4096, 24, 512
+    gdev = synthetic.make_generator(args.seed + 9, dev)
+    xs = [synthetic.order(synthetic.wkv7_vectors((T, H, 64), gdev)) for _ in range(L)]
+    lay = RWKV7StateLayout(n_layer=L, hidden_size=H * 64, num_heads=H, head_dim=64,
+                           head_v_dim=64, dtype=torch.bfloat16)
+    bank = RWKV7StateBank(lay, num_slots=1, device=dev)
+    run = WKV7Runner(bank, prefill_chunk=chunk)
+    fla_x = [[x.unsqueeze(0) for x in layer] for layer in xs]
+    ys = [torch.empty((T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    ids_t = torch.tensor([1], dtype=torch.int32, device=dev)
+    cu_t = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
+    slot = {"wkv": 1, "shift": 1}
+
+    def fla():
+        states = [None] * L
+        for c in range(0, T, chunk):
+            for l in range(L):
+                _, states[l] = ops.chunk_rwkv7(*(x[:, c:c + chunk] for x in fla_x[l]),
+                                               initial_state=states[l], output_final_state=True)
+        return states
+
+    def runner():
+        bank.zero_slots(slot)
+        run.prefill(xs, slot)
+
+    rows = bank.num_slots + 1
+    esz = 2 * H * 64  # bytes per token row of one input
+
+    def raw():
+        for c in range(0, T, chunk):
+            for l in range(L):
+                launcher.prefill(bank.wkv[l].data_ptr(), rows, H, ids_t.data_ptr(),
+                                 cu_t.data_ptr(), 1, chunk,
+                                 [x.data_ptr() + c * esz for x in xs[l]],
+                                 ys[l].data_ptr() + c * esz, 1 if c == 0 else 0)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        out = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append((e0.elapsed_time(e1), 1e3 * (time.perf_counter() - t0)))
+        return statistics.median(o[0] for o in out), statistics.median(o[1] for o in out)
+
+    res = {"tokens": T, "layers": L, "heads": H, "prefill_chunk": chunk, "launches": L * T // chunk}
+    for name, fn in (("fla", fla), ("runner", runner), ("launcher", raw)):
+        ms, wall = timed(fn)
+        res[f"{name}_ms"] = ms
+        res[f"{name}_wall_ms"] = wall
+        res[f"{name}_tokens_per_s"] = T / (ms * 1e-3)
+        log(f"request prefill ({T} tokens, chunk {chunk}, {L} layers, H={H}) via {name}: "
+            f"{ms:.3f} ms ({T / (ms * 1e-3):.3e} tok/s), host wall {wall:.3f} ms")
+    del xs, fla_x, ys, bank
     torch.cuda.empty_cache()
     return res
 
@@ -1000,13 +1081,15 @@ def main() -> int:
               "mixed_ragged": lambda: bench_mixed(torch, dev, args, launcher),
               "decode_graph": lambda: bench_decode_graph(torch, dev, args),
               "state_store": lambda: bench_store(torch, dev, args),
-              "time_mix": lambda: bench_time_mix(torch, dev, args)}[args.only]
+              "time_mix": lambda: bench_time_mix(torch, dev, args),
+              "request_prefill": lambda: bench_request_prefill(torch, dev, args, launcher)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
     dec = bench_decode(torch, dev, args, launcher)
     pre = bench_prefill(torch, dev, args, launcher)
     extra = {}
     if not args.no_extra:
+        extra["request_prefill"] = bench_request_prefill(torch, dev, args, launcher)
         extra["fla_decode"] = bench_fla_decode(torch, dev, args)
         extra["fork_decode_7b"] = bench_fork_decode_7b(torch, dev, args, launcher)
         extra["mixed_ragged"] = bench_mixed(torch, dev, args, launcher)

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 9
+#define WKV7_ABI_VERSION 10
 
 #define WKV7_OK 0
 #define WKV7_ERR_ARG (-1)       /* null pointer, negative size, bad enum */
@@ -149,7 +149,8 @@ int wkv7_decode_into(const float *state_in, int64_t in_rows, const int32_t *in_i
  *   r..b          [total_tokens, H, 64] bf16, 16-byte aligned (else WKV7_ERR_SHAPE)
  *   y             [total_tokens, H, 64], dtype per y_dtype; 8-byte aligned for
  *                 bf16, 16-byte for fp32 (whole rows are stored as vectors;
- *                 else WKV7_ERR_SHAPE)
+ *                 else WKV7_ERR_SHAPE); a sequence whose slot id is outside
+ *                 [0, num_rows) gets y = 0 and its state is not touched
  *
  * Decay range: the chunked form scales operands by exp(+-G) with G a sum of
  * up to 16 consecutive log-decays, so every w must be >= -5 (exp(80) is
@@ -185,7 +186,11 @@ int wkv7_prefill_varlen(float *wkv_layer, int64_t num_rows, int32_t H,
  * WKV7_RUN_* bits, NULL = all 0) select the initial state, zero k and v, and
  * redirect y to y_alt (same shape, dtype and alignment as y) and the state to
  * state_alt [alt_rows, H, 64, 64] fp32. A run's rows must be distinct from
- * every other run's.
+ * every other run's. With state_in [in_rows, H, 64, 64] fp32 (NULL = none),
+ * a run that starts from a stored state (no zero or identity flag, zero_init
+ * 0) reads it from state_in row in_ids[run] (in_ids NULL: row `run`, which
+ * needs in_rows >= nseq) instead of its slot row; its final state still goes
+ * to the slot row. Rejected rows give y = 0 as in wkv7_prefill_varlen.
  */
 int wkv7_prefill_runs(float *wkv_layer, int64_t num_rows, int32_t H,
                       const int32_t *slot_ids, const int32_t *cu_seqlens,
@@ -194,7 +199,43 @@ int wkv7_prefill_runs(float *wkv_layer, int64_t num_rows, int32_t H,
                       const uint16_t *v, const uint16_t *a, const uint16_t *b,
                       void *y, int32_t y_dtype, int32_t zero_init, float scale,
                       const int32_t *run_flags, const int32_t *cu_alt, int32_t n_primary,
-                      float *state_alt, int64_t alt_rows, void *y_alt, void *stream);
+                      float *state_alt, int64_t alt_rows, void *y_alt,
+                      const float *state_in, int64_t in_rows, const int32_t *in_ids,
+                      void *stream);
+
+/*
+ * Chunked prefill with the state read from one tensor and written to another:
+ * sequence s reads its initial state from state_in[in_ids[s]] and writes its
+ * final state to state_out[out_ids[s]] (both [rows, H, 64, 64] fp32). The
+ * arithmetic is wkv7_prefill_varlen's; with state_in == state_out and
+ * in_ids == out_ids it is that call.
+ *
+ * Replaces fla's chunk_rwkv7 as the reference's model layer calls it for
+ * every prefill chunk (seq_len >= 64, wkvm/models/rwkv7.py:108-113; reached
+ * from RWKV7Runner.prefill, wkvm/runner/runner.py:52-61):
+ * chunk_rwkv7(r, w, k, v, a, b, initial_state=, output_final_state=,
+ * cu_seqlens=) reads initial_state and returns a new final_state tensor, so
+ * no copy of the state is needed.
+ *
+ *   state_in   NULL = zero initial state (fla's initial_state=None)
+ *   in_ids     [nseq] int32 (device), or NULL: sequence s reads row s
+ *   state_out  NULL = no final state written (output_final_state=False)
+ *   out_ids    [nseq] int32 (device), or NULL: sequence s writes row s; must
+ *              be distinct, and no sequence may write a state row another
+ *              sequence reads
+ *   in_rows, out_rows   rows of each tensor (at least nseq where its ids are
+ *              NULL, else WKV7_ERR_SHAPE); a sequence with an id outside
+ *              [0, rows) gets y = 0 and no state write
+ *   H, cu_seqlens, seq_order, nseq, total_tokens, r..b, y, y_dtype, scale
+ *              as wkv7_prefill_varlen (same alignment rules and decay range)
+ * Ids without their tensor are WKV7_ERR_ARG.
+ */
+int wkv7_prefill_into(const float *state_in, int64_t in_rows, const int32_t *in_ids,
+                      float *state_out, int64_t out_rows, const int32_t *out_ids, int32_t H,
+                      const int32_t *cu_seqlens, const int32_t *seq_order, int32_t nseq,
+                      int64_t total_tokens, const uint16_t *r, const uint16_t *w,
+                      const uint16_t *k, const uint16_t *v, const uint16_t *a,
+                      const uint16_t *b, void *y, int32_t y_dtype, float scale, void *stream);
 
 /*
  * The state chain of a segmented prefill, per (sequence, head), in segment

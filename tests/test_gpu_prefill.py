@@ -117,25 +117,40 @@ def test_cfg2_full_size_zero_init(dev):
     assert bool((gpool[others] == 7.0).all())
 
 
-def test_repeated_runs_are_bit_identical(dev):
-    """The same ragged batch (slot state in, fp32 y) run six times gives
-    bit-identical y and final states every time: no result may depend on
-    timing (matrix-core results read back by vector instructions before they
-    are ready, LDS reads racing a tick's writes)."""
-    H, S = 32, 16
-    lens = [4096, 4001, 17, 1, 100, 2000, 33, 3000]
-    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+@pytest.mark.parametrize("batch", ["ragged", "cfg4_rows", "segmented"])
+def test_repeated_runs_are_bit_identical(dev, batch):
+    """The same batch (slot state in, fp32 y) run six times gives bit-identical
+    y and final states every time: no result may depend on timing
+    (matrix-core results read back by vector instructions before they are
+    ready, LDS reads racing a tick's writes). Three batches: eight ragged
+    sequences; config 4's prefill rows (64 lengths uniform in [1, 2048] at the
+    1.5B head count, longest first); and the segmented form (runs from zero
+    and identity state, the chain and the correction) on few long sequences.
+    Re-entry determinism is what the reference relies on when a preempted
+    request resumes from its slot (wkvm/runner/runner.py:30-33)."""
+    H, S = 32, 72
     gen = synthetic.make_generator(5)
-    vecs = synthetic.wkv7_vectors((cu[-1], H, 64), gen)
-    xs = [vecs[n].to(dev) for n in "rwkvab"]
-    pool0 = torch.zeros((S + 1, H, 64, 64))
-    pool0[1:] = synthetic.initial_states((S, H, 64, 64), gen)
-    pool0 = pool0.to(dev)
+    if batch == "cfg4_rows":
+        lens = torch.randint(1, 2049, (64,), generator=gen).tolist()
+    elif batch == "segmented":
+        lens = [4096, 3000, 17]
+    else:
+        lens = [4096, 4001, 17, 1, 100, 2000, 33, 3000]
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    gdev = synthetic.make_generator(6, dev)  # config 4's ~65k tokens are drawn on the GPU
+    vecs = synthetic.wkv7_vectors((cu[-1], H, 64), gdev)
+    xs = [vecs[n] for n in "rwkvab"]
+    pool0 = torch.zeros((S + 1, H, 64, 64), device=dev)
+    pool0[1:] = synthetic.initial_states((S, H, 64, 64), gdev)
     ids = list(range(1, len(lens) + 1))
     ref = None
     for rep in range(6):
         pool = pool0.clone()
-        y = ops.wkv7_prefill_varlen(pool, ids, cu, *xs, out_dtype=torch.float32)
+        if batch == "segmented":
+            y = ops.wkv7_prefill_segments(pool, ids, cu, *xs, segments=4,
+                                          out_dtype=torch.float32)
+        else:
+            y = ops.wkv7_prefill_varlen(pool, ids, cu, *xs, out_dtype=torch.float32)
         torch.cuda.synchronize()
         if ref is None:
             ref = (y, pool)
@@ -149,8 +164,8 @@ def test_chunk_split_invariance_through_the_slot(dev):
     the slot (prefill_chunk 64, 100 and 4096), as a preempted request's would.
     Chunks on the kernel's 16-token sub-chunk grid (64) reproduce the one-call
     result bit for bit; other chunks (100) shift the grid, and the operands the
-    kernel takes as one bf16 each (A^, T, h in A^ h) then round differently, so
-    they agree to the parity bar (measured 2.9e-4 on the state, 2.1e-4 on y)."""
+    kernel takes as one bf16 each (A^, T) then round differently, so they
+    agree to the parity bar."""
     lay = RWKV7StateLayout(n_layer=2, hidden_size=512, num_heads=8, head_dim=64, head_v_dim=64,
                            dtype=torch.bfloat16)
     T = 700
@@ -200,6 +215,109 @@ def test_fla_signatures(dev):
     assert h3[1].abs().sum().item() == 0.0
     _, none = ops.chunk_rwkv7(*xs, output_final_state=False)
     assert none is None
+
+
+def test_chunk_rwkv7_cfg2_shape_out_of_place(dev):
+    """chunk_rwkv7 at config 2's shape (8 x 4096 tokens, H = 32) from an
+    initial state: the state is read from initial_state and written to a new
+    final_state by one kernel launch (no copy of the state), both against the
+    float64 oracle; initial_state keeps its bytes, and output_final_state=False
+    runs the same y with no state written (wkvm/models/rwkv7.py:108-109)."""
+    B, T, H = 8, 4096, 32
+    gen = synthetic.make_generator(53)
+    vecs = synthetic.wkv7_vectors((B, T, H, 64), gen)
+    h0 = synthetic.initial_states((B, H, 64, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    h0d = h0.to(dev)
+    o, hT = ops.chunk_rwkv7(*xs, initial_state=h0d, output_final_state=True)
+    torch.cuda.synchronize()
+    assert hT.data_ptr() != h0d.data_ptr()
+    assert torch.equal(h0d.cpu(), h0)  # initial_state is only read
+    cu = np.arange(B + 1) * T
+    flat = [U.bits(vecs[n].reshape(B * T, H, 64)) for n in "rwkvab"]
+    y_ref, h_ref = O.scan_bf16(cu, *flat, pool=h0.numpy(), slot_ids=list(range(B)))
+    y_cmp = O.round_f64_to_bf16(y_ref)
+    hv, yv = U.f64(hT), U.f64(o).reshape(B * T, H, 64)
+    eh = max(U.rel_l2(hv[s], h_ref[s]) for s in range(B))
+    ey = max(U.rel_l2(yv[s * T:(s + 1) * T], y_cmp[s * T:(s + 1) * T]) for s in range(B))
+    print(f"chunk_rwkv7 cfg2 shape: worst state rel L2 {eh:.2e}, y {ey:.2e}")
+    assert eh <= REL_L2 and ey <= REL_L2
+    o2, none = ops.chunk_rwkv7(*xs, initial_state=h0d, output_final_state=False)
+    torch.cuda.synchronize()
+    assert none is None and torch.equal(o2, o)
+
+
+def test_prefill_into_rows_and_in_place(dev):
+    """wkv7_prefill_into: sequences read states from permuted rows of one
+    tensor and write them to other rows of another; the result equals the
+    in-place slot prefill bit for bit, and the same tensor with in_ids ==
+    out_ids is the in-place call. No state_in means zero state; no state_out
+    writes nothing."""
+    H, S = 4, 9
+    lens = [100, 0, 1, 333]
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    gen = synthetic.make_generator(57)
+    src = synthetic.initial_states((S, H, 64, 64), gen).to(dev)
+    vecs = [x.to(dev) for x in synthetic.order(synthetic.wkv7_vectors((cu[-1], H, 64), gen))]
+    in_ids, out_ids = [5, 0, 8, 2], [1, 7, 3, 6]
+    dst = torch.full((S, H, 64, 64), 3.0, device=dev)
+    y = ops.wkv7_prefill_into(src, dst, cu, *vecs, in_ids=in_ids, out_ids=out_ids,
+                              out_dtype=torch.float32)
+    pool = src.clone()
+    y_ref = ops.wkv7_prefill_varlen(pool, in_ids, cu, *vecs, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    assert torch.equal(dst[out_ids], pool[in_ids])
+    assert torch.equal(dst[7], src[0])  # the empty sequence's state passes through
+    assert bool((dst[[0, 2, 4, 5, 8]] == 3.0).all())
+    same = src.clone()
+    y2 = ops.wkv7_prefill_into(same, same, cu, *vecs, in_ids=in_ids, out_ids=in_ids,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y_ref) and torch.equal(same, pool)
+    zero = torch.zeros_like(src)
+    y_zero_ref = ops.wkv7_prefill_varlen(zero, [1, 2, 3, 4], cu, *vecs, out_dtype=torch.float32)
+    y3 = ops.wkv7_prefill_into(None, None, cu, *vecs, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y3, y_zero_ref)
+    with pytest.raises(ValueError, match="reads"):
+        ops.wkv7_prefill_into(same, same, cu, *vecs, in_ids=[0, 1, 2, 3], out_ids=[1, 2, 3, 4])
+
+
+def test_rejected_device_slot_ids_zero_the_prefill_y(dev):
+    """A device slot id the kernel's bounds check rejects leaves that
+    sequence's state untouched and writes y = 0 for its tokens (as the decode
+    step does), so a caller's uninitialised output never leaks; the other
+    sequences are unaffected. Same for wkv7_prefill_into's in and out ids."""
+    H, S = 2, 6
+    lens = [40, 100, 17]
+    cu = [0, 40, 140, 157]
+    gen = synthetic.make_generator(309)
+    pool = synthetic.initial_states((S + 1, H, 64, 64), gen).to(dev)
+    before = pool.clone()
+    vecs = [x.to(dev) for x in synthetic.order(synthetic.wkv7_vectors((cu[-1], H, 64), gen))]
+    for y_dtype in (torch.bfloat16, torch.float32):
+        pool.copy_(before)
+        bad = torch.tensor([2, S + 1, 4], dtype=torch.int32, device=dev)
+        y = torch.full((cu[-1], H, 64), 5.0, dtype=y_dtype, device=dev)
+        ops.wkv7_prefill_varlen(pool, bad, torch.tensor(cu, dtype=torch.int32, device=dev),
+                                *vecs, out=y)
+        ref = before.clone()
+        y_ok = ops.wkv7_prefill_varlen(ref, [2, 4], [0, 40, 57],
+                                       *(torch.cat([x[0:40], x[140:157]]) for x in vecs),
+                                       out_dtype=y_dtype)
+        torch.cuda.synchronize()
+        assert not torch.any(y[40:140])
+        assert torch.equal(y[0:40], y_ok[0:40]) and torch.equal(y[140:157], y_ok[40:57])
+        assert torch.equal(pool, ref)
+    dst = torch.zeros_like(before)
+    y2 = torch.full((cu[-1], H, 64), 5.0, device=dev)
+    ops.wkv7_prefill_into(before, dst, cu, *vecs, out=y2,
+                          in_ids=torch.tensor([1, -1, 3], dtype=torch.int32, device=dev),
+                          out_ids=torch.tensor([1, 2, 99], dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert torch.any(y2[0:40]) and not torch.any(y2[40:157])
+    assert torch.any(dst[1]) and not torch.any(dst[2:])
 
 
 def test_prefill_argument_errors(dev):
@@ -377,6 +495,36 @@ def test_decay_extremes_and_scale(dev, pattern):
         sl = slice(int(cu[s]), int(cu[s + 1]))
         assert U.rel_l2(U.f64(y[sl]), y_ref[sl]) <= REL_L2
         assert U.rel_l2(U.f64(gpool[ids[s]]), h_ref[s]) <= REL_L2
+
+
+@pytest.mark.parametrize("pattern", ["channels", "tokens"])
+def test_slow_decay_long_sequence(dev, pattern):
+    """Where state accumulates most: 4,096 tokens with no decay (w = 0) on half
+    the key channels, or on every third token, from slot state, at the unit
+    scale of the shipped fast path. The operands the kernel rounds to one bf16
+    (A^, T) must keep the state and y within the parity bar over the whole
+    length, per sequence; h as one bf16 in the A^ h product did not (y 1.7e-3
+    against the bf16-rounded oracle, state 8e-4, on the "channels" pattern)."""
+    H, S = 4, 4
+    lens = [4096, 4096]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    T = int(cu[-1])
+    gen = synthetic.make_generator(79)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    ids = [3, 1]
+    vecs = synthetic.wkv7_vectors((T, H, 64), gen)
+    wmax = -synthetic.DECAY_SCALE
+    if pattern == "channels":
+        w = torch.where(torch.arange(64) % 2 == 0, 0.0, wmax).expand(T, H, 64)
+    else:
+        w = torch.where(torch.arange(T) % 3 == 0, 0.0, wmax)[:, None, None].expand(T, H, 64)
+    vecs["w"] = w.to(torch.bfloat16).contiguous()
+    gpool = pool.to(dev)
+    y = ops.wkv7_prefill_varlen(gpool, ids, cu.tolist(), *(vecs[n].to(dev) for n in "rwkvab"))
+    torch.cuda.synchronize()
+    eh, ey = _check(pool.numpy(), ids, cu, U.vec_bits(vecs), gpool, y, zero_init=False)
+    print(f"slow decay ({pattern}), 4096 tokens: worst state rel L2 {eh:.2e}, y {ey:.2e}")
 
 
 @pytest.mark.parametrize("zero_init", [False, True])

@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_header_symbol():
     lib = _lib.load()
     for name in _lib.header_symbols():
         assert hasattr(lib, name), name
-    assert lib.wkv7_abi_version() == _lib.WKV7_ABI_VERSION == 9
+    assert lib.wkv7_abi_version() == _lib.WKV7_ABI_VERSION == 10
 
 
 def test_a_library_of_another_abi_version_is_refused(monkeypatch):
@@ -305,20 +305,43 @@ def test_segment_entry_points_reject_bad_arguments():
     E_ARG, E_SHAPE = _lib.WKV7_ERR_ARG, _lib.WKV7_ERR_SHAPE
     # runs: n_primary beyond nseq, secondary runs without ranges, misaligned inputs
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
-                                 3, None, 0, None, None) == E_ARG
+                                 3, None, 0, None, None, 0, None, None) == E_ARG
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, p, None,
-                                 1, p, 2, None, None) == E_ARG
+                                 1, p, 2, None, None, 0, None, None) == E_ARG
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, p + 2, *[p] * 5, p, 0, 0, 1.0,
-                                 None, None, 2, None, 0, None, None) == E_SHAPE
+                                 None, None, 2, None, 0, None, None, 0, None, None) == E_SHAPE
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 0, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
-                                 0, None, 0, None, None) == 0
+                                 0, None, 0, None, None, 0, None, None) == 0
     # y and y_alt are stored as whole-row vectors: 8-byte (bf16) / 16-byte (fp32) aligned
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 4, 0, 0, 1.0, None,
-                                 None, 2, None, 0, None, None) == E_SHAPE
+                                 None, 2, None, 0, None, None, 0, None, None) == E_SHAPE
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 8, 1, 0, 1.0, None,
-                                 None, 2, None, 0, None, None) == E_SHAPE
+                                 None, 2, None, 0, None, None, 0, None, None) == E_SHAPE
     assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None,
-                                 None, 2, None, 0, p + 2, None) == E_SHAPE
+                                 None, 2, None, 0, p + 2, None, 0, None, None) == E_SHAPE
+    # runs reading initial states from state_in: ids without the tensor, too few rows
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
+                                 2, None, 0, None, None, 0, p, None) == E_ARG
+    assert lib.wkv7_prefill_runs(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p, 0, 0, 1.0, None, None,
+                                 2, None, 0, None, p, 1, None, None) == E_SHAPE
+    # out-of-place prefill: ids without their tensor, too few rows without ids,
+    # bad y dtype, misaligned y; zero state in and no state out is a valid shape
+    assert lib.wkv7_prefill_into(None, 0, p, p, 4, None, 2, p, None, 2, 8, *[p] * 6, p, 0, 1.0,
+                                 None) == E_ARG
+    assert lib.wkv7_prefill_into(p, 4, None, None, 0, p, 2, p, None, 2, 8, *[p] * 6, p, 0, 1.0,
+                                 None) == E_ARG
+    assert lib.wkv7_prefill_into(p, 1, None, p, 4, None, 2, p, None, 2, 8, *[p] * 6, p, 0, 1.0,
+                                 None) == E_SHAPE
+    assert lib.wkv7_prefill_into(None, 0, None, p, 1, None, 2, p, None, 2, 8, *[p] * 6, p, 0,
+                                 1.0, None) == E_SHAPE
+    assert lib.wkv7_prefill_into(None, 0, None, None, 0, None, 2, p, None, 2, 8, *[p] * 6, p, 4,
+                                 1.0, None) == E_ARG
+    assert lib.wkv7_prefill_into(None, 0, None, None, 0, None, 2, None, None, 2, 8, *[p] * 6, p,
+                                 0, 1.0, None) == E_ARG
+    assert lib.wkv7_prefill_into(None, 0, None, None, 0, None, 2, p, None, 2, 8, *[p] * 6, p + 4,
+                                 0, 1.0, None) == E_SHAPE
+    assert lib.wkv7_prefill_into(None, 0, None, None, 0, None, 2, p, None, 0, 8, *[p] * 6, p, 0,
+                                 1.0, None) == 0
     assert lib.wkv7_prefill_varlen(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 2, 0, 0, 1.0,
                                    None) == E_SHAPE
     assert lib.wkv7_prefill_varlen(p, 4, 2, p, p, None, 2, 8, *[p] * 6, p + 8, 1, 0, 1.0,

@@ -18,7 +18,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "wkv7.h")
 
 # The ABI this binding is written for (WKV7_ABI_VERSION of include/wkv7.h);
 # a library built from other sources is refused at load.
-WKV7_ABI_VERSION = 9
+WKV7_ABI_VERSION = 10
 
 WKV7_OK = 0
 WKV7_ERR_ARG = -1
@@ -68,7 +68,10 @@ SIGNATURES = {
         _i32, _f32, _vp]),
     "wkv7_prefill_runs": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
-        _i32, _f32, _vp, _vp, _i32, _vp, _i64, _vp, _vp]),
+        _i32, _f32, _vp, _vp, _i32, _vp, _i64, _vp, _vp, _i64, _vp, _vp]),
+    "wkv7_prefill_into": (ctypes.c_int, [
+        _vp, _i64, _vp, _vp, _i64, _vp, _i32, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp,
+        _vp, _vp, _i32, _f32, _vp]),
     "wkv7_segment_chain": (ctypes.c_int, [
         _vp, _i64, _i32, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp]),
     "wkv7_segment_correct": (ctypes.c_int, [

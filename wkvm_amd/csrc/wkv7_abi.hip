@@ -8,7 +8,7 @@ extern "C" const char* wkv7_strerror(int code) {
     case WKV7_OK: return "success";
     case WKV7_ERR_ARG: return "invalid argument (null pointer, negative size or bad enum)";
     case WKV7_ERR_SHAPE: return "unsupported layout (row size beyond the slot stride, or inputs not 16-byte aligned)";
-    case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_prefill_workspace_bytes()";
+    case WKV7_ERR_WORKSPACE: return "workspace or staging buffer missing, or smaller than the entry point needs";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -36,12 +36,12 @@
 //
 // Precision: MFMA operands that are not exact bf16 inputs are split into bf16
 // hi + lo parts, a product formed as hi*hi + hi*lo + lo*hi with fp32
-// accumulation (~2^-16 relative per product), except three that enter as one
-// bf16 each: A^, T (solved in fp32, then rounded) and h in the A^ h product.
-// Those cost ~2^-9 relative on P only; over 4096 tokens the worst final state
-// of a config-2 batch is 2.8e-4 relative L2 from the all-split form (y 1.8e-4)
-// and ~7 % of the time. Products with the exact bf16 v need one MFMA per term
-// pair. Operand layouts below
+// accumulation (~2^-16 relative per product), except two that enter as one
+// bf16 each: A^ and T (solved in fp32, then rounded). Those cost ~2^-9
+// relative on P only. h enters the A^ h product split as well: as one bf16
+// it left a 4096-token run with no decay on half the key channels at 8e-4
+// relative L2 on y and state (1.5e-4 split). Products with the exact bf16 v
+// need one MFMA per term pair. Operand layouts below
 // (v_mfma_f32_16x16x32_bf16, lane l, li = l%16, lg = l/16): A lane holds
 // A[li][8lg..8lg+7] of a 32-wide k block, B lane holds B[8lg..8lg+7][li], the
 // accumulator holds D[4lg..4lg+3][li]. Contractions over 16 tokens put
@@ -495,7 +495,8 @@ __device__ __forceinline__ f32x4 stage_state(const Shared& sm, f32x4 (&h)[4], in
   f32x4 Z = mma32(mrk, vv, zero);  // M_rk V
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    X = mma32(ah[kb], hbh[kb], X);  // + A^ h (A^ and h as one bf16 each)
+    X = mma32(ah[kb], hbl[kb], X);  // + A^ h (A^ as one bf16, h split)
+    X = mma32(ah[kb], hbh[kb], X);
     Z = mma32x3(rh[kb], rl[kb], hbh[kb], hbl[kb], Z);  // + R^ h
   }
   uint2 xh, xl;
@@ -731,11 +732,13 @@ __device__ __forceinline__ void operand_loop(Shared& sm, const Load& ld, const S
 // and the inverse's serial substitution chain runs beside the state chain
 // instead of after it in the same wave. All kinds pass the same sequence of
 // barriers: three fill ticks, then one per sub-chunk.
-// Per-run options of wkv7_prefill_runs (all absent for wkv7_prefill_varlen).
-// Runs [0, n_primary) take their token range from cu_seqlens; run
-// n_primary + i takes [ranges[2i], ranges[2i+1]). Flags select the initial
-// state (slot row, zero or identity), zero k and v, and redirect y and the
-// final state.
+// Per-run options of wkv7_prefill_runs and wkv7_prefill_into (all absent for
+// wkv7_prefill_varlen). Runs [0, n_primary) take their token range from
+// cu_seqlens; run n_primary + i takes [ranges[2i], ranges[2i+1]). Flags select
+// the initial state (slot row, zero or identity), zero k and v, and redirect y
+// and the final state. With state_in set, a run that starts from a stored
+// state reads it from state_in (row in_ids[run], or row `run` when in_ids is
+// null) instead of its slot row.
 struct Runs {
   const int32_t* flags;   // [nseq] or null
   const int32_t* cu_alt;  // [2 (nseq - n_primary)] begin/end pairs, or null
@@ -743,11 +746,33 @@ struct Runs {
   float* state_alt;       // [alt_rows, H, 64, 64]
   int64_t alt_rows;
   void* y_alt;            // like y
+  const float* state_in;  // [in_rows, H, 64, 64] or null
+  const int32_t* in_ids;  // [nseq] or null
+  int64_t in_rows;
 };
 
+// y = 0 for every token of a run whose state rows were rejected (as the decode
+// step does for a rejected row): 16 lanes per 128-byte (bf16) or 256-byte
+// (fp32) row.
+template <bool kF32Out>
+__device__ __forceinline__ void zero_y(void* y, const SeqGeom& g) {
+  const int col = threadIdx.x & 15;
+  for (int64_t t = g.t_beg + (threadIdx.x >> 4); t < g.t_end; t += kThreads / 16) {
+    const int64_t o = t * g.tstride + g.hoff;
+    if constexpr (kF32Out)
+      reinterpret_cast<float4*>(static_cast<float*>(y) + o)[col] = make_float4(0.f, 0.f, 0.f, 0.f);
+    else
+      reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + o)[col] = make_uint2(0u, 0u);
+  }
+}
+
+// wkv (with slot_ids) is where the final states go, and the initial states
+// come from unless runs.state_in, zero_init or a run flag says otherwise; a
+// null wkv writes no final state (slot_ids may then be null too: run s is
+// row s).
 template <bool kF32Out, bool kBuf, bool kScaled>
 __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
-    float* __restrict__ wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
+    float* wkv, int64_t num_rows, int H, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ seq_order, int nseq,
     Inputs in, void* __restrict__ y, int64_t total_tokens, int zero_init, float scale, Runs runs) {
   __shared__ Shared sm;
@@ -762,9 +787,6 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   const int64_t seq = seq_order ? int64_t(seq_order[pos]) : pos;
   if (seq < 0 || seq >= nseq) return;  // uniform: the whole block leaves
   const int fl = runs.flags ? runs.flags[seq] : 0;
-  const int64_t slot = slot_ids[seq];
-  const int64_t rows_of = (fl & WKV7_RUN_STATE_ALT) ? runs.alt_rows : num_rows;
-  if (slot < 0 || slot >= rows_of) return;  // uniform: the whole block leaves
   const int32_t* cu = cu_seqlens;
   int64_t ci = seq;
   if (seq >= runs.n_primary) {  // only with cu_alt (n_primary = nseq otherwise)
@@ -777,24 +799,43 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   g.tstride = int64_t(H) * kHead;
   g.hoff = head * kHead;
   const int64_t n_sub = (g.t_end - g.t_beg + kSub - 1) / kSub;
+  void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
+
+  // State rows of this run: checked before any state access (uniform).
+  const bool state_alt = fl & WKV7_RUN_STATE_ALT;
+  float* out_base = state_alt ? runs.state_alt : wkv;
+  const int64_t out_rows = state_alt ? runs.alt_rows : num_rows;
+  const int64_t slot = slot_ids ? int64_t(slot_ids[seq]) : seq;
+  const bool from_eye = fl & WKV7_RUN_INIT_IDENTITY;
+  const bool from_zero = !from_eye && (zero_init || (fl & WKV7_RUN_INIT_ZERO));
+  const bool from_in = !from_eye && !from_zero && runs.state_in;
+  const int64_t in_row = from_in ? (runs.in_ids ? int64_t(runs.in_ids[seq]) : seq) : 0;
+  const bool rows_ok = (!out_base || (slot >= 0 && slot < out_rows)) &&
+                       (!from_in || (in_row >= 0 && in_row < runs.in_rows)) &&
+                       (from_eye || from_zero || from_in || out_base);
+  if (!rows_ok) {
+    zero_y<kF32Out>(yb, g);
+    return;  // uniform: the whole block leaves
+  }
 
   if (wave < 4) {
     // ---- state chain ----
     const int li = lane & 15, lg = lane >> 4;
-    float* hbase = ((fl & WKV7_RUN_STATE_ALT) ? runs.state_alt : wkv) +
-                   (slot * H + head) * (kHead * kHead);
+    const int64_t tile = kHead * kHead;
+    const float* hsrc = from_in    ? runs.state_in + (in_row * H + head) * tile
+                        : out_base ? out_base + (slot * H + head) * tile
+                                   : nullptr;  // not read: zero or identity start
+    float* hdst = out_base ? out_base + (slot * H + head) * tile : nullptr;
     const int col0 = kSub * wave;  // this wave's value columns [col0, col0 + 16)
     // State columns of this wave as four 16x16 accumulator tiles (key blocks jb).
     f32x4 h[4];
-    const bool from_zero = zero_init || (fl & WKV7_RUN_INIT_ZERO);
-    const bool from_eye = fl & WKV7_RUN_INIT_IDENTITY;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int j = 16 * jb + 4 * lg + rr;
         h[jb][rr] = from_eye ? (j == col0 + li ? 1.f : 0.f)
-                             : from_zero ? 0.f : hbase[j * kHead + col0 + li];
+                             : from_zero ? 0.f : hsrc[j * kHead + col0 + li];
       }
     if (n_sub > 0) {
       if constexpr (kBuf) end_tick();  // the row loads' fourth fill tick
@@ -807,11 +848,13 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
         end_tick();
       }
     }
+    if (hdst) {
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+      for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        hbase[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
+        for (int rr = 0; rr < 4; ++rr)
+          hdst[(16 * jb + 4 * lg + rr) * kHead + col0 + li] = h[jb][rr];
+    }
   } else if (wave >= 8 + kOpWaves) {
     // ---- T of the next sub-chunk ----
     // The substitution is one serial chain of 14 broadcast + fma steps; a
@@ -834,7 +877,6 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
   } else if (wave >= 4 + kOpWaves) {
     if (n_sub > 0) {
       const int part = wave - 4 - kOpWaves;
-      void* yb = (fl & WKV7_RUN_Y_ALT) ? runs.y_alt : y;
       if constexpr (kBuf) end_tick();
       end_tick();
       stage_scores(sm, 0, lane, part);
@@ -933,7 +975,7 @@ extern "C" int wkv7_prefill_varlen(float* wkv_layer, int64_t num_rows, int32_t H
   if (!wkv_layer || !slot_ids || !cu_seqlens) return WKV7_ERR_ARG;
   if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
   if (!inputs_aligned(r, w, k, v, a, b) || !y_aligned(y, y_dtype)) return WKV7_ERR_SHAPE;
-  const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr};
+  const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr, nullptr, nullptr, 0};
   return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
                         total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,
                         runs, stream);
@@ -947,8 +989,11 @@ extern "C" int wkv7_prefill_runs(float* wkv_layer, int64_t num_rows, int32_t H,
                                  int32_t y_dtype, int32_t zero_init, float scale,
                                  const int32_t* run_flags, const int32_t* cu_alt,
                                  int32_t n_primary, float* state_alt, int64_t alt_rows,
-                                 void* y_alt, void* stream) {
+                                 void* y_alt, const float* state_in, int64_t in_rows,
+                                 const int32_t* in_ids, void* stream) {
   if (nseq < 0 || H < 1 || num_rows < 1 || total_tokens < 0 || alt_rows < 0) return WKV7_ERR_ARG;
+  if (in_rows < 0 || (state_in && in_rows < 1) || (in_ids && !state_in)) return WKV7_ERR_ARG;
+  if (state_in && !in_ids && in_rows < nseq) return WKV7_ERR_SHAPE;
   if (n_primary < 0 || n_primary > nseq) return WKV7_ERR_ARG;
   if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
   if (nseq == 0) return WKV7_OK;
@@ -959,8 +1004,32 @@ extern "C" int wkv7_prefill_runs(float* wkv_layer, int64_t num_rows, int32_t H,
   if (!inputs_aligned(r, w, k, v, a, b) || !y_aligned(y, y_dtype) ||
       (y_alt && !y_aligned(y_alt, y_dtype)))
     return WKV7_ERR_SHAPE;
-  const Runs runs{run_flags, cu_alt, n_primary, state_alt, alt_rows, y_alt ? y_alt : y};
+  const Runs runs{run_flags, cu_alt,   n_primary, state_alt, alt_rows,
+                  y_alt ? y_alt : y, state_in, in_ids,    in_rows};
   return prefill_launch(wkv_layer, num_rows, H, slot_ids, cu_seqlens, seq_order, nseq,
                         total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype, zero_init, scale,
                         runs, stream);
+}
+
+extern "C" int wkv7_prefill_into(const float* state_in, int64_t in_rows, const int32_t* in_ids,
+                                 float* state_out, int64_t out_rows, const int32_t* out_ids,
+                                 int32_t H, const int32_t* cu_seqlens, const int32_t* seq_order,
+                                 int32_t nseq, int64_t total_tokens, const uint16_t* r,
+                                 const uint16_t* w, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* a, const uint16_t* b, void* y, int32_t y_dtype,
+                                 float scale, void* stream) {
+  if (nseq < 0 || H < 1 || total_tokens < 0 || in_rows < 0 || out_rows < 0) return WKV7_ERR_ARG;
+  if (y_dtype != WKV7_Y_BF16 && y_dtype != WKV7_Y_F32) return WKV7_ERR_ARG;
+  if ((in_ids && !state_in) || (out_ids && !state_out)) return WKV7_ERR_ARG;
+  if (nseq == 0) return WKV7_OK;
+  if (!cu_seqlens) return WKV7_ERR_ARG;
+  if (total_tokens > 0 && (!r || !w || !k || !v || !a || !b || !y)) return WKV7_ERR_ARG;
+  if ((state_in && !in_ids && in_rows < nseq) || (state_out && !out_ids && out_rows < nseq))
+    return WKV7_ERR_SHAPE;
+  if (!inputs_aligned(r, w, k, v, a, b) || !y_aligned(y, y_dtype)) return WKV7_ERR_SHAPE;
+  // no state_in: zero initial state; no state_out: no final state written
+  const Runs runs{nullptr, nullptr, nseq, nullptr, 0, nullptr, state_in, in_ids, in_rows};
+  return prefill_launch(state_out, state_out ? out_rows : 0, H, out_ids, cu_seqlens, seq_order,
+                        nseq, total_tokens, Inputs{r, w, k, v, a, b}, y, y_dtype,
+                        state_in ? 0 : 1, scale, runs, stream);
 }

@@ -62,7 +62,8 @@ class RWKV7StateLayout:
         """Same derivation as wkvm/models/rwkv7.py:57-70 from an fla config."""
         value_dims = set(config.value_dim)
         if len(value_dims) != 1:
-            raise NotImplementedError(f"heterogeneous value_dim: {config.value_dim}")
+            raise NotImplementedError(
+                f"every layer must share one value width; config.value_dim = {config.value_dim}")
         if config.attn is not None:
             raise NotImplementedError("hybrid attn layers are not supported")
         return cls(
@@ -91,7 +92,8 @@ class RWKV7StateLayout:
 
     @property
     def shift_shape(self) -> tuple[int, ...]:
-        # 2 token-shift caches per layer: [0] attn conv_state, [1] ffn_state.
+        # One hidden-size row per family; the bank keeps two families per
+        # layer (index 0: the time-mix shift, index 1: the channel-mix shift).
         return (self.hidden_size,)
 
     def state_spec(self) -> ModelStateSpec:

@@ -318,6 +318,79 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
     return y
 
 
+def wkv7_prefill_into(state_in: torch.Tensor | None, state_out: torch.Tensor | None,
+                      cu_seqlens, r, w, k, v, a, b, *, in_ids=None, out_ids=None,
+                      scale: float = 1.0, out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype = torch.bfloat16,
+                      seq_order: torch.Tensor | None = None) -> torch.Tensor:
+    """Ragged prefill with the state read from ``state_in`` and written to
+    ``state_out`` (each ``[rows, H, 64, 64]`` fp32, or None: a zero initial
+    state / no final state written). Sequence ``s`` reads
+    ``state_in[in_ids[s]]`` and writes ``state_out[out_ids[s]]``; ``None`` ids
+    mean row ``s``. This is fla's ``chunk_rwkv7`` contract (initial_state ->
+    a new final_state) without a copy of the state. Returns ``y [T, H, 64]``.
+    """
+    _require_cuda(r, "prefill.r")
+    if r.dim() != 3:
+        raise ValueError(f"prefill inputs must be [T, H, 64], got {tuple(r.shape)}")
+    T, H = int(r.shape[0]), int(r.shape[1])
+    dev = r.device
+    xs = _check_vectors((r, w, k, v, a, b), (T, H, HEAD_SIZE), dev, "prefill")
+    lst = _host_cu(cu_seqlens, T) if not (isinstance(cu_seqlens, torch.Tensor)
+                                          and cu_seqlens.is_cuda) else None
+    nseq = len(lst) - 1 if lst is not None else int(cu_seqlens.shape[0]) - 1
+    in_rows = _state_tensor(state_in, H, dev, "state_in")
+    out_rows = _state_tensor(state_out, H, dev, "state_out")
+    if in_ids is not None and state_in is None:
+        raise ValueError("in_ids without state_in")
+    if out_ids is not None and state_out is None:
+        raise ValueError("out_ids without state_out")
+    for t, ids, n in ((state_in, in_ids, "state_in"), (state_out, out_ids, "state_out")):
+        if t is not None and ids is None and t.shape[0] < nseq:
+            raise ValueError(f"{n} has {t.shape[0]} rows for {nseq} sequences")
+    if state_in is not None and state_out is not None and _overlaps(state_in, state_out):
+        if state_in.data_ptr() != state_out.data_ptr():
+            raise ValueError("state_in and state_out overlap at different offsets")
+        if not all(isinstance(x, _IDS) or x is None for x in (in_ids, out_ids)):
+            raise ValueError("overlapping state tensors need host ids (checked here)")
+        src = list(range(nseq)) if in_ids is None else [int(i) for i in in_ids]
+        dst = list(range(nseq)) if out_ids is None else [int(i) for i in out_ids]
+        if src != dst and set(src) & set(dst):
+            raise ValueError("a sequence writes a state row that another sequence reads")
+    d_in = None if in_ids is None else device_ids(in_ids, in_rows, dev, "in_ids", distinct=False)
+    d_out = None if out_ids is None else device_ids(out_ids, out_rows, dev, "out_ids",
+                                                    distinct=True)
+    for ids in (d_in, d_out):
+        if ids is not None and int(ids.shape[0]) != nseq:
+            raise ValueError(f"{int(ids.shape[0])} ids for {nseq} sequences")
+    if lst is not None:
+        both = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
+        cu = both[:nseq + 1]
+        if seq_order is None:
+            seq_order = both[nseq + 1:]
+    else:
+        if cu_seqlens.dtype != torch.int32:
+            raise ValueError("device cu_seqlens must be int32")
+        cu = cu_seqlens
+    if seq_order is not None and not (isinstance(seq_order, torch.Tensor) and seq_order.is_cuda
+                                      and seq_order.dtype == torch.int32
+                                      and tuple(seq_order.shape) == (nseq,)):
+        raise ValueError("seq_order must be a device int32 tensor of nseq entries")
+    code = _y_code(out.dtype if out is not None else out_dtype)
+    y = _out(out, (T, H, HEAD_SIZE), out_dtype if out is None else out.dtype, dev, "out")
+    if y.data_ptr() % (16 if y.dtype == torch.float32 else 8):
+        raise ValueError("out must be 8-byte aligned (bf16) or 16-byte aligned (fp32): the "
+                         "kernel stores whole rows as vectors")
+    if nseq == 0:
+        return y
+    rc = _lib.load().wkv7_prefill_into(_ptr(state_in), in_rows, _ptr(d_in), _ptr(state_out),
+                                       out_rows, _ptr(d_out), H, cu.data_ptr(), _ptr(seq_order),
+                                       nseq, T, *[x.data_ptr() for x in xs], y.data_ptr(), code,
+                                       float(scale), _stream_ptr(dev))
+    _lib.check(rc, "wkv7_prefill_into")
+    return y
+
+
 def segment_cuts(length: int, segments: int) -> list[int]:
     """Cut points ``0 = c_0 < ... < c_G = length`` of one sequence into at most
     ``segments`` pieces, each a multiple of 16 tokens except the last."""
@@ -331,7 +404,8 @@ def segment_cuts(length: int, segments: int) -> list[int]:
 def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, v, a, b, *,
                           segments: int, zero_init: bool = False, scale: float = 1.0,
                           out: torch.Tensor | None = None,
-                          out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                          out_dtype: torch.dtype = torch.bfloat16,
+                          state_in: torch.Tensor | None = None) -> torch.Tensor:
     """``wkv7_prefill_varlen`` with each sequence cut into up to ``segments``
     pieces that run side by side, for batches of few, long sequences (one
     sequence of H heads keeps only H compute units busy).
@@ -345,7 +419,10 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
     ``wkv7_segment_correct`` writes y = y0 + q H_in for every token, in fp32,
     rounded once to ``out_dtype``. Results match the one-pass scan to fp32
     rounding. ``slot_ids`` and ``cu_seqlens`` are host sequences; the plan is
-    one upload, the scratch four tensors from the caching allocator."""
+    one upload, the scratch four tensors from the caching allocator. With
+    ``state_in`` (``[nseq, H, 64, 64]`` fp32) sequence ``s`` starts from
+    ``state_in[s]`` instead of its slot row; the final state still goes to
+    the slot."""
     rows, H = _check_pool(wkv_layer)
     dev = wkv_layer.device
     if segments < 1:
@@ -358,16 +435,22 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
     cu = _host_cu(cu_seqlens, T)
     if len(cu) != nseq + 1:
         raise ValueError(f"cu_seqlens has {len(cu)} entries for {nseq} sequences")
+    in_rows = _state_tensor(state_in, H, dev, "state_in")
+    if state_in is not None and (zero_init or in_rows < nseq):
+        raise ValueError("state_in needs zero_init False and a row per sequence")
     dtype = out.dtype if out is not None else out_dtype
     code = _y_code(dtype)
     y = _out(out, (T, H, HEAD_SIZE), dtype, dev, "out")
-    empty = [ids[s] for s in range(nseq) if cu[s] == cu[s + 1]]
+    empty = [s for s in range(nseq) if cu[s] == cu[s + 1]]
     if zero_init and empty:
-        slot_zero(wkv_layer, empty, slot_dim=0)
+        slot_zero(wkv_layer, [ids[s] for s in empty], slot_dim=0)
+    if state_in is not None and empty:
+        # an empty sequence's final state is its initial state
+        slot_copy(wkv_layer, [ids[s] for s in empty], state_in, empty, slot_dim=0)
     if T == 0:
         return y
     L = _lib
-    run_slot, run_flags, prim_cu = [], [], [0]
+    run_slot, run_flags, prim_cu, run_src = [], [], [0], []
     alt_slot, alt_flags, alt_pairs = [], [], []
     seq_tab, seg_tab, blk = [], [], []
     n_alt = nsegs = 0
@@ -382,6 +465,7 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
             continue
         cuts = segment_cuts(end - beg, segments)
         run_slot.append(ids[s])
+        run_src.append(s)
         run_flags.append(L.WKV7_RUN_INIT_ZERO if zero_init else 0)
         prim_cu.append(beg + cuts[1])
         blocks(beg, beg + cuts[1], -1)
@@ -389,6 +473,7 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
         for g in range(1, len(cuts) - 1):
             b_, e_ = beg + cuts[g], beg + cuts[g + 1]
             run_slot.append(n_alt)
+            run_src.append(0)  # zero start: state_in is not read
             run_flags.append(L.WKV7_RUN_INIT_ZERO | L.WKV7_RUN_STATE_ALT)
             prim_cu.append(e_)
             alt_slot.append(n_alt + 1)
@@ -407,13 +492,13 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
     lens += [alt_pairs[2 * i + 1] - alt_pairs[2 * i] for i in range(len(alt_slot))]
     order = sorted(range(nruns), key=lambda i: -lens[i])
     parts = [run_slot + alt_slot, run_flags + alt_flags, prim_cu, alt_pairs or [0, 0], order,
-             seq_tab or [0, 0, 0], seg_tab or [0, 0], blk]
+             seq_tab or [0, 0, 0], seg_tab or [0, 0], blk, run_src + [0] * len(alt_slot)]
     plan = torch.tensor([x for p in parts for x in p], dtype=torch.int32, device=dev)
     views, at = [], 0
     for p in parts:
         views.append(plan[at:at + len(p)])
         at += len(p)
-    v_ids, v_flags, v_cu, v_pairs, v_order, v_seq, v_seg, v_blk = views
+    v_ids, v_flags, v_cu, v_pairs, v_order, v_seq, v_seg, v_blk, v_src = views
     y0 = torch.empty((T, H, HEAD_SIZE), dtype=torch.float32, device=dev)
     q = torch.empty_like(y0) if nsegs else y0
     alt = torch.empty((max(n_alt, 1), H, HEAD_SIZE, HEAD_SIZE), dtype=torch.float32, device=dev)
@@ -424,7 +509,8 @@ def wkv7_prefill_segments(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k
                                v_order.data_ptr(), nruns, T, *[x.data_ptr() for x in xs],
                                y0.data_ptr(), _lib.WKV7_Y_F32, 0, float(scale),
                                v_flags.data_ptr(), v_pairs.data_ptr(), n_primary,
-                               alt.data_ptr(), n_alt, q.data_ptr(), stream)
+                               alt.data_ptr(), n_alt, q.data_ptr(), _ptr(state_in), in_rows,
+                               v_src.data_ptr() if state_in is not None else None, stream)
     _lib.check(rc, "wkv7_prefill_runs")
     if nsegs:
         rc = lib.wkv7_segment_chain(wkv_layer.data_ptr(), rows, H, alt.data_ptr(), n_alt,
@@ -905,8 +991,8 @@ def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqle
     """fla's wkv-op contract: ``[B, T, H, 64]`` inputs (or ``[1, T_total, H,
     64]`` packed by ``cu_seqlens``), ``initial_state`` read, a new
     ``final_state`` returned. One token per sequence runs the decode kernel
-    out of place (initial_state -> final_state, no copy); longer sequences run
-    the chunked scan on a copy of initial_state."""
+    and longer sequences the chunked scan, both out of place (initial_state ->
+    final_state, no copy of the state)."""
     if head_first:
         r, w, k, v, a, b = (x.transpose(1, 2) for x in (r, w, k, v, a, b))
     _require_cuda(r, "r")
@@ -937,21 +1023,23 @@ def _seq_op(r, w, k, v, a, b, scale, initial_state, output_final_state, cu_seqle
         y = wkv7_decode_into(state, final, *flat, scale=scale, out_dtype=r.dtype)
         o = y.reshape(B, T, H, K)
         return (o.transpose(1, 2) if head_first else o), final
-    if state is None:
-        pool = torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
-    else:
-        pool = state.clone() if state is initial_state else state
     G = auto_segments(H, lens, dev)
     if G > 1:  # few long sequences: run their segments side by side
+        # the segment chain needs the final states in a pool of its own
+        pool = torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
         y = wkv7_prefill_segments(pool, list(range(nseq)), host_cu, *flat, segments=G,
-                                  zero_init=state is None, scale=scale, out_dtype=r.dtype)
+                                  zero_init=state is None, scale=scale, out_dtype=r.dtype,
+                                  state_in=state)
+        final = pool if output_final_state else None
     else:
-        y = wkv7_prefill_varlen(pool, list(range(nseq)), host_cu, *flat,
-                                zero_init=state is None, scale=scale, out_dtype=r.dtype)
+        # state read from initial_state, written to a new final_state: no copy
+        final = (torch.empty((nseq, H, K, K), dtype=torch.float32, device=dev)
+                 if output_final_state else None)
+        y = wkv7_prefill_into(state, final, host_cu, *flat, scale=scale, out_dtype=r.dtype)
     o = y.reshape(B, T, H, K)
     if head_first:
         o = o.transpose(1, 2)
-    return o, (pool if output_final_state else None)
+    return o, final
 
 
 def fused_recurrent_rwkv7(r, w, k, v, a, b, scale: float = 1.0, initial_state=None,
