@@ -454,7 +454,10 @@ def bench_request_prefill(torch, dev, args, launcher):
                            head_v_dim=64, dtype=torch.bfloat16)
     bank = RWKV7StateBank(lay, num_slots=1, device=dev)
     run = WKV7Runner(bank, prefill_chunk=chunk)
-    fla_x = [[x.unsqueeze(0) for x in layer] for layer in xs]
+    # the model layer hands chunk_rwkv7 one slice's [1, chunk, H, 64] tensors
+    # (wkvm/models/rwkv7.py:108-113); cut them before the timed region
+    fla_x = [[[x.unsqueeze(0)[:, c:c + chunk] for x in layer] for layer in xs]
+             for c in range(0, T, chunk)]
     ys = [torch.empty((T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(L)]
     ids_t = torch.tensor([1], dtype=torch.int32, device=dev)
     cu_t = torch.tensor([0, chunk], dtype=torch.int32, device=dev)
@@ -462,10 +465,10 @@ def bench_request_prefill(torch, dev, args, launcher):
 
     def fla():
         states = [None] * L
-        for c in range(0, T, chunk):
+        for sl in fla_x:
             for l in range(L):
-                _, states[l] = ops.chunk_rwkv7(*(x[:, c:c + chunk] for x in fla_x[l]),
-                                               initial_state=states[l], output_final_state=True)
+                _, states[l] = ops.chunk_rwkv7(*sl[l], initial_state=states[l],
+                                               output_final_state=True)
         return states
 
     def runner():

@@ -23,6 +23,7 @@ Error behaviour mirrors the reference: invalid arguments raise ``ValueError``
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from typing import Iterable, Sequence
 
 import numpy as np
@@ -260,6 +261,29 @@ def _host_cu(cu, T: int) -> list[int]:
     return lst
 
 
+_PLANS: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_PLAN_CACHE_SIZE = 256
+
+
+def _device_plan(lst: list[int], dev: torch.device) -> torch.Tensor:
+    """``cu_seqlens`` followed by the longest-first start order, as one device
+    int32 tensor. Cached per (device, offsets): the fla-signature callers
+    repeat the same offsets on every call (one request per call in fixed
+    prefill_chunk slices, wkvm/runner/runner.py:52-61), and the upload is the
+    largest part of such a call's host time. The tensor is complete when it
+    is returned (a blocking copy from pageable memory) and only ever read."""
+    key = (dev.index, tuple(lst))
+    plan = _PLANS.get(key)
+    if plan is None:
+        plan = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
+        _PLANS[key] = plan
+        if len(_PLANS) > _PLAN_CACHE_SIZE:
+            _PLANS.popitem(last=False)
+    else:
+        _PLANS.move_to_end(key)
+    return plan
+
+
 def longest_first(cu: Sequence[int]) -> list[int]:
     """Sequence order for a ragged prefill launch: longest first (ties in
     index order), which packs the per-(sequence, head) workgroups onto the
@@ -295,7 +319,7 @@ def wkv7_prefill_varlen(wkv_layer: torch.Tensor, slot_ids, cu_seqlens, r, w, k, 
         lst = _host_cu(cu_seqlens, T)
         if len(lst) != nseq + 1:
             raise ValueError(f"cu_seqlens has {len(lst)} entries for {nseq} sequences")
-        both = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
+        both = _device_plan(lst, dev)
         cu = both[:nseq + 1]
         if seq_order is None:
             seq_order = both[nseq + 1:]
@@ -364,7 +388,7 @@ def wkv7_prefill_into(state_in: torch.Tensor | None, state_out: torch.Tensor | N
         if ids is not None and int(ids.shape[0]) != nseq:
             raise ValueError(f"{int(ids.shape[0])} ids for {nseq} sequences")
     if lst is not None:
-        both = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
+        both = _device_plan(lst, dev)
         cu = both[:nseq + 1]
         if seq_order is None:
             seq_order = both[nseq + 1:]
