@@ -117,15 +117,16 @@ def test_cfg2_full_size_zero_init(dev):
     assert bool((gpool[others] == 7.0).all())
 
 
-@pytest.mark.parametrize("batch", ["ragged", "cfg4_rows", "segmented"])
+@pytest.mark.parametrize("batch", ["ragged", "cfg4_rows", "segmented", "one_request"])
 def test_repeated_runs_are_bit_identical(dev, batch):
     """The same batch (slot state in, fp32 y) run six times gives bit-identical
     y and final states every time: no result may depend on timing
     (matrix-core results read back by vector instructions before they are
-    ready, LDS reads racing a tick's writes). Three batches: eight ragged
+    ready, LDS reads racing a tick's writes). Four batches: eight ragged
     sequences; config 4's prefill rows (64 lengths uniform in [1, 2048] at the
-    1.5B head count, longest first); and the segmented form (runs from zero
-    and identity state, the chain and the correction) on few long sequences.
+    1.5B head count, longest first); the segmented form (runs from zero
+    and identity state, the chain and the correction) on few long sequences;
+    and one 4096-token request, which runs on the quarter-head kernel.
     Re-entry determinism is what the reference relies on when a preempted
     request resumes from its slot (wkvm/runner/runner.py:30-33)."""
     H, S = 32, 72
@@ -134,6 +135,8 @@ def test_repeated_runs_are_bit_identical(dev, batch):
         lens = torch.randint(1, 2049, (64,), generator=gen).tolist()
     elif batch == "segmented":
         lens = [4096, 3000, 17]
+    elif batch == "one_request":
+        lens = [4096]
     else:
         lens = [4096, 4001, 17, 1, 100, 2000, 33, 3000]
     cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
@@ -320,6 +323,41 @@ def test_rejected_device_slot_ids_zero_the_prefill_y(dev):
     assert torch.any(dst[1]) and not torch.any(dst[2:])
 
 
+@pytest.mark.parametrize("zero_init", [False, True])
+@pytest.mark.parametrize("y_dtype", [torch.bfloat16, torch.float32])
+def test_quarter_heads_bit_identical_to_whole_heads(dev, zero_init, y_dtype):
+    """A launch that would keep at most a quarter of the compute units busy
+    (4 x sequences x heads <= CUs) runs each (sequence, head) on four
+    workgroups, one per 16 value columns, each repeating the operand, score
+    and inverse work. The same sequences launched beside enough empty ones to
+    fill the GPU run one workgroup per pair. Both give the same bits, and
+    both match the oracle."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 4
+    lens = [700, 1, 33, 0, 256, 64]
+    assert 4 * len(lens) * H <= cus
+    n_pad = cus // (4 * H) + 1 - len(lens)
+    S = len(lens) + n_pad + 2
+    gen = synthetic.make_generator(83)
+    pool = torch.zeros((S + 1, H, 64, 64))
+    pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    vecs = synthetic.wkv7_vectors((cu[-1], H, 64), gen)
+    xs = [vecs[n].to(dev) for n in "rwkvab"]
+    ids = list(range(1, len(lens) + 1))
+    few = pool.to(dev)
+    y_few = ops.wkv7_prefill_varlen(few, ids, cu, *xs, zero_init=zero_init, out_dtype=y_dtype)
+    full = pool.to(dev)
+    ids_full = ids + list(range(len(lens) + 1, len(lens) + 1 + n_pad))
+    assert 4 * len(ids_full) * H > cus
+    y_full = ops.wkv7_prefill_varlen(full, ids_full, cu + [cu[-1]] * n_pad, *xs,
+                                     zero_init=zero_init, out_dtype=y_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y_few, y_full)
+    assert torch.equal(few[:len(lens) + 1], full[:len(lens) + 1])
+    _check(pool.numpy(), ids, np.array(cu), U.vec_bits(vecs), few, y_few, zero_init)
+
+
 def test_prefill_argument_errors(dev):
     pool = torch.zeros((5, 2, 64, 64), device=dev)
     vecs = synthetic.order(synthetic.wkv7_vectors((10, 2, 64), synthetic.make_generator(0),
@@ -426,14 +464,17 @@ def test_mixed_step_concurrent_equals_serial(dev):
         assert torch.equal(a, b)
 
 
-def test_large_batch_uses_the_64bit_input_path(dev):
-    """A batch whose input bytes exceed 31-bit offsets (H = 64, 262,444 tokens)
-    runs the operand waves' global-load path instead of the buffer-resource
-    one; the first (checked) sequence must match the oracle there too. The
-    second sequence is zero input and only makes the batch large."""
-    H, S = 64, 4
-    lens = [300, 262144]
-    cu = [0, 300, 300 + 262144]
+@pytest.mark.parametrize("H", [64, 8])
+def test_large_batch_uses_the_64bit_input_path(dev, H):
+    """A batch whose input bytes exceed 31-bit offsets runs the operand waves'
+    global-load path instead of the buffer-resource one; the first (checked)
+    sequence must match the oracle there too. The second sequence is zero
+    input and only makes the batch large: 262,144 tokens at H = 64 (one
+    workgroup per head) or 2,097,152 at H = 8 (few heads: the quarter-head
+    kernel)."""
+    S = 4
+    lens = [300, (1 << 24) // H]
+    cu = [0, lens[0], lens[0] + lens[1]]
     gen = synthetic.make_generator(191)
     pool = torch.zeros((S + 1, H, 64, 64))
     pool[1:] = synthetic.initial_states((S, H, 64, 64), gen)

@@ -22,7 +22,7 @@ OBJ_DIR = os.path.join(PKG_DIR, "_build")
 ARCH = "gfx950"
 
 SOURCES = ("wkv7_abi.hip", "wkv7_slot.hip", "wkv7_decode.hip", "wkv7_prefill.hip",
-           "wkv7_mix.hip", "wkv7_segments.hip", "wkv7_proj.hip")
+           "wkv7_prefill_quarter.hip", "wkv7_mix.hip", "wkv7_segments.hip", "wkv7_proj.hip")
 
 # Packed-fp32 VALU forms are disabled for every kernel (v_pk_{add,mul,fma}_f32
 # have shown silent wrong results on these boxes); the host pass warns that it
