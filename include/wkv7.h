@@ -346,7 +346,10 @@ int wkv7_slot_transfer(int32_t direction, void *host, void *base, int64_t outer_
  *   shift_rows   one layer and family of bank.shift: num_rows rows of D bf16,
  *                row_stride elements apart (bank.shift[l, f] has row_stride D)
  *   slot_ids     [nseq] int32 (device), distinct
- *   cu_seqlens   [nseq + 1] int32 (device), as for wkv7_prefill_varlen
+ *   cu_seqlens   [nseq + 1] int32 (device), as for wkv7_prefill_varlen; NULL
+ *                for a decode batch (sequence t is token t: nseq must equal
+ *                total_tokens, else WKV7_ERR_ARG), which spares every token
+ *                one dependent read before its slot id
  *   mix          [n_mix, D] bf16 (x_r, x_w, x_k, x_v, x_a, x_g for the
  *                attention mixer; x_k for the channel mixer)
  *   out          n_mix outputs of [total_tokens, D] bf16, out_stride elements

@@ -294,6 +294,8 @@ def test_timemix_abi_rejects_bad_arguments():
                                     None) == ERR_SHAPE
     assert lib.wkv7_token_shift_mix(p, 4, 64, p, 3, 32, p, p, 1, p, 1, p, 256, None) == ERR_ARG
     assert lib.wkv7_token_shift_mix(p, 0, 64, p, 3, 64, p, p, 1, p, 1, p, 0, None) == 0
+    # no offsets (one token per sequence) with fewer sequences than tokens
+    assert lib.wkv7_token_shift_mix(p, 4, 64, p, 3, 64, p, None, 3, p, 1, p, 256, None) == ERR_ARG
     # inputs: v_lora without v_first, null k, misaligned output
     assert lib.wkv7_time_mix_inputs(2, 1, p, p, p, p, p, None, p, p, p, p, p, p, p,
                                     None) == ERR_ARG

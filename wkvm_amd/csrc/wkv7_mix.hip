@@ -41,10 +41,9 @@ __device__ __forceinline__ float el(const Bf8& v, int e) {
 }
 
 // Sequence of token t: the largest s with cu[s] <= t (empty sequences have
-// cu[s] == cu[s+1] and are skipped by taking the largest such s).
-// The last sequence s with cu[s] <= t (the one holding token t when t is
-// inside a sequence). Decode batches have one token per sequence, so s = t is
-// tried first: one load pair instead of a binary search of dependent loads,
+// cu[s] == cu[s+1] and are skipped by taking the largest such s), which holds
+// token t when t is inside a sequence. s = t is tried first (one token per
+// sequence): one load pair instead of a binary search of dependent loads,
 // which dominated the latency of a small launch.
 __device__ __forceinline__ int seq_of(const int32_t* cu, int nseq, int64_t t) {
   const int g = int(t < int64_t(nseq - 1) ? t : int64_t(nseq - 1));
@@ -63,9 +62,14 @@ __global__ __launch_bounds__(kMixThreads) void token_shift_mix_kernel(
     const int32_t* __restrict__ cu, int nseq, const uint16_t* __restrict__ mix, int n_mix,
     uint16_t* __restrict__ out, int64_t out_stride) {
   for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
-    const int s = seq_of(cu, nseq, t);
-    const int64_t beg = max(int64_t(cu[s]), int64_t(0)), end = min(int64_t(cu[s + 1]), T);
-    if (t < beg || t >= end) continue;  // tokens outside every sequence (uniform)
+    int s = int(t);  // no offsets: one token per sequence
+    int64_t beg = t, end = t + 1;
+    if (cu) {
+      s = seq_of(cu, nseq, t);
+      beg = max(int64_t(cu[s]), int64_t(0));
+      end = min(int64_t(cu[s + 1]), T);
+      if (t < beg || t >= end) continue;  // tokens outside every sequence (uniform)
+    }
     const bool first = t == beg;
     const int64_t slot = first ? int64_t(slot_ids[s]) : -1;
     const bool cached = slot >= 0 && slot < num_rows;
@@ -208,8 +212,8 @@ extern "C" int wkv7_token_shift_mix(const uint16_t* x, int64_t total_tokens, int
   if (total_tokens < 0 || D < 1 || nseq < 0 || n_mix < 0 || num_rows < 1 || row_stride < D)
     return WKV7_ERR_ARG;
   if (total_tokens == 0 || nseq == 0) return WKV7_OK;
-  if (!x || !shift_rows || !slot_ids || !cu_seqlens || (n_mix > 0 && (!mix || !out)))
-    return WKV7_ERR_ARG;
+  if (!x || !shift_rows || !slot_ids || (n_mix > 0 && (!mix || !out))) return WKV7_ERR_ARG;
+  if (!cu_seqlens && int64_t(nseq) != total_tokens) return WKV7_ERR_ARG;
   if (n_mix > 1 && out_stride < total_tokens * int64_t(D)) return WKV7_ERR_ARG;
   if ((D & 7) || (row_stride & 7) || (out_stride & 7) || !aligned16(x) || !aligned16(shift_rows) ||
       (n_mix > 0 && (!aligned16(mix) || !aligned16(out))))

@@ -345,9 +345,9 @@ struct TileShape {
   int bm, bn;
 };
 
-// Tile shapes, largest first (fewest re-reads of x and w); measured on the
-// MI355X inside HIP graphs.
-constexpr TileShape kShapes[] = {{64, 64}, {32, 32}};
+// Tile shapes (fewer re-reads of x and w per output the larger the tile);
+// measured on the MI355X inside HIP graphs.
+constexpr TileShape kShapes[] = {{64, 64}, {32, 32}, {128, 64}};
 
 int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) {
   int64_t tiles = 0;
@@ -399,24 +399,33 @@ struct Plan {
 };
 
 Plan make_plan(int64_t m, const wkv7_proj_group* gs, int ng, int cus) {
-  // 64 x 64 tiles (8 waves, 2-stage ring of 128-wide k stages) when they
-  // give every compute unit about 1.5 workgroups or more; else 32 x 32 tiles
-  // (4 waves, 4-stage ring).
-  Plan p{1, 1, 0};
-  int64_t tiles = count_tiles(m, gs, ng, kShapes[1]);
-  if (count_tiles(m, gs, ng, kShapes[0]) * 2 >= int64_t(cus) * 3) {
-    p.shape = 0;
-    tiles = count_tiles(m, gs, ng, kShapes[0]);
-  }
-  // At most one workgroup per two units and long k: split k so that about two
-  // workgroups per unit each walk at least 8 stages. (With more tiles the
-  // partials' extra traffic and second launch cost more than they save.)
   int kmin = gs[0].k;
   int64_t cols = 0;
   for (int i = 0; i < ng; ++i) {
     kmin = std::min(kmin, gs[i].k);
     cols += gs[i].n;
   }
+  // The launch reads (BM + BN) rows of k per tile from L2, which bounds it
+  // at a few hundred rows. 128 x 64 tiles (8 waves, 3-stage ring of 128-wide
+  // k stages: 144 KiB of LDS, so one workgroup per compute unit) when k is
+  // long (8 stages or more) and they fill three quarters of the units or
+  // more in one round: a unit then reads 192 rows instead of up to twice 128
+  // (the 1.5B first stage at 256 rows: 20.1 against 22.7 us). Else 64 x 64
+  // tiles (8 waves, 2-stage ring) when they give every unit about 1.5
+  // workgroups or more; else 32 x 32 tiles (4 waves, 4-stage ring).
+  Plan p{1, 1, 0};
+  int64_t tiles = count_tiles(m, gs, ng, kShapes[1]);
+  const int64_t t128 = count_tiles(m, gs, ng, kShapes[2]);
+  if (kmin >= 1024 && t128 * 4 >= int64_t(cus) * 3 && t128 <= int64_t(cus)) {
+    p.shape = 2;
+    tiles = t128;
+  } else if (count_tiles(m, gs, ng, kShapes[0]) * 2 >= int64_t(cus) * 3) {
+    p.shape = 0;
+    tiles = count_tiles(m, gs, ng, kShapes[0]);
+  }
+  // At most one workgroup per two units and long k: split k so that about two
+  // workgroups per unit each walk at least 8 stages. (With more tiles the
+  // partials' extra traffic and second launch cost more than they save.)
   const int nk = (kmin + 63) / 64;
   if (tiles * 2 <= int64_t(cus) && nk >= 16) {
     int64_t parts = (2 * int64_t(cus) + tiles / 2) / tiles;
@@ -523,6 +532,7 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
   float* ws = static_cast<float*>(workspace);
   hipStream_t s = as_stream(stream);
   if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  if (p.shape == 2) return launch<128, 64, 3, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
   return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
 }
 
@@ -544,5 +554,6 @@ extern "C" int wkv7_proj_grouped_noalloc(int64_t m, const wkv7_proj_group* group
   }
   hipStream_t s = as_stream(stream);
   if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  if (p.shape == 2) return launch<128, 64, 3, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
   return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
 }

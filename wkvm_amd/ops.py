@@ -770,10 +770,11 @@ def token_shift_mix(x: torch.Tensor, shift_rows: torch.Tensor, slot_ids, mix: to
 
     ``x [T, D]`` bf16 (the mixer's input), ``shift_rows [rows, D]`` bf16 (one
     layer and family of ``bank.shift``, e.g. ``bank.shift[l, 0]``), ``mix
-    [M, D]`` bf16. ``cu_seqlens=None`` means one token per slot (decode).
-    Returns ``out [M, T, D]``: ``bf16(x + bf16(prev - x) * mix[m])`` with
-    prev the previous token, or the slot's row for a sequence's first token;
-    each sequence's last row of ``x`` becomes its slot's row (in place)."""
+    [M, D]`` bf16. ``cu_seqlens=None`` means one token per slot (decode; the
+    kernel then gets no offsets). Returns ``out [M, T, D]``:
+    ``bf16(x + bf16(prev - x) * mix[m])`` with prev the previous token, or the
+    slot's row for a sequence's first token; each sequence's last row of ``x``
+    becomes its slot's row (in place)."""
     _require_cuda(shift_rows, "shift_rows")
     if shift_rows.dtype != torch.bfloat16 or shift_rows.dim() != 2 or shift_rows.stride(1) != 1:
         raise ValueError("shift_rows must be a bf16 [rows, D] view with unit channel stride")
@@ -791,7 +792,13 @@ def token_shift_mix(x: torch.Tensor, shift_rows: torch.Tensor, slot_ids, mix: to
         raise ValueError("x, shift_rows and mix must share a device")
     if D % 8 or shift_rows.stride(0) % 8 or shift_rows.data_ptr() % 16:
         raise ValueError("D and the shift row stride must be multiples of 8 (16-byte rows)")
-    ids, cu, nseq = seq_plan(slot_ids, cu_seqlens, rows, T, dev)
+    if cu_seqlens is None:  # decode: sequence t is token t, no offsets
+        ids = device_ids(slot_ids, rows, dev, "slot_ids")
+        nseq, cu = int(ids.shape[0]), None
+        if nseq != T:
+            raise ValueError(f"{nseq} slots for {T} decode tokens")
+    else:
+        ids, cu, nseq = seq_plan(slot_ids, cu_seqlens, rows, T, dev)
     y = _out(out, (M, T, D), torch.bfloat16, dev, "out")
     if y.dtype != torch.bfloat16 or y.data_ptr() % 16:
         raise ValueError("out must be a 16-byte aligned bf16 tensor")
@@ -799,7 +806,7 @@ def token_shift_mix(x: torch.Tensor, shift_rows: torch.Tensor, slot_ids, mix: to
         return y
     rc = _lib.load().wkv7_token_shift_mix(x.data_ptr(), T, D, shift_rows.data_ptr(), rows,
                                           int(shift_rows.stride(0)), ids.data_ptr(),
-                                          cu.data_ptr(), nseq, mix.data_ptr(), M, y.data_ptr(),
+                                          _ptr(cu), nseq, mix.data_ptr(), M, y.data_ptr(),
                                           T * D, _stream_ptr(dev))
     _lib.check(rc, "wkv7_token_shift_mix")
     return y

@@ -157,8 +157,9 @@ class RWKV7TimeMix:
         W, l, H = self.w, self.layer_idx, self.layout.num_heads
         if l > 0 and v_first is None:
             raise ValueError("layers after the first need v_first")
-        xr, xw, xk, xv, xa, xg = ops.token_shift_mix(x, bank.shift[l, 0], batch.slot_ids,
-                                                     W["mix"], batch.cu_seqlens)
+        xr, xw, xk, xv, xa, xg = ops.token_shift_mix(
+            x, bank.shift[l, 0], batch.slot_ids, W["mix"],
+            None if batch.decode else batch.cu_seqlens)
         if batch.tokens <= self.PROJ_MAX_ROWS:
             return self._forward_grouped(bank, batch, v_first, zero_init,
                                          (xr, xw, xk, xv, xa, xg))
