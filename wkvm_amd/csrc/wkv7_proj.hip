@@ -347,7 +347,7 @@ struct TileShape {
 
 // Tile shapes (fewer re-reads of x and w per output the larger the tile);
 // measured on the MI355X inside HIP graphs.
-constexpr TileShape kShapes[] = {{64, 64}, {32, 32}, {128, 64}};
+constexpr TileShape kShapes[] = {{64, 64}, {32, 32}, {128, 64}, {64, 32}};
 
 int64_t count_tiles(int64_t m, const wkv7_proj_group* gs, int ng, TileShape sh) {
   int64_t tiles = 0;
@@ -406,19 +406,25 @@ Plan make_plan(int64_t m, const wkv7_proj_group* gs, int ng, int cus) {
     cols += gs[i].n;
   }
   // The launch reads (BM + BN) rows of k per tile from L2, which bounds it
-  // at a few hundred rows. 128 x 64 tiles (8 waves, 3-stage ring of 128-wide
-  // k stages: 144 KiB of LDS, so one workgroup per compute unit) when k is
-  // long (8 stages or more) and they fill three quarters of the units or
-  // more in one round: a unit then reads 192 rows instead of up to twice 128
-  // (the 1.5B first stage at 256 rows: 20.1 against 22.7 us). Else 64 x 64
-  // tiles (8 waves, 2-stage ring) when they give every unit about 1.5
-  // workgroups or more; else 32 x 32 tiles (4 waves, 4-stage ring).
+  // at a few hundred rows. With long k (8 stages or more), the largest tile
+  // of one workgroup per compute unit that fills three quarters of the units
+  // or more in one round: 128 x 64 (8 waves, 3-stage ring of 128-wide k
+  // stages, 144 KiB of LDS), then 64 x 32 (4 waves, 4-stage ring, 96 KiB).
+  // A unit then reads 192 or 96 rows instead of twice 128 or 64 (the 1.5B
+  // first stage at 256 rows: 20.1 against 22.7 us; o_proj 10.6 against 11.3).
+  // Else 64 x 64 tiles (8 waves, 2-stage ring) when they give every unit
+  // about 1.5 workgroups or more; else 32 x 32 tiles (4 waves, 4-stage ring).
   Plan p{1, 1, 0};
   int64_t tiles = count_tiles(m, gs, ng, kShapes[1]);
+  auto fills = [&](int64_t t) { return t * 4 >= int64_t(cus) * 3 && t <= int64_t(cus); };
   const int64_t t128 = count_tiles(m, gs, ng, kShapes[2]);
-  if (kmin >= 1024 && t128 * 4 >= int64_t(cus) * 3 && t128 <= int64_t(cus)) {
+  const int64_t t6432 = count_tiles(m, gs, ng, kShapes[3]);
+  if (kmin >= 1024 && fills(t128)) {
     p.shape = 2;
     tiles = t128;
+  } else if (kmin >= 1024 && fills(t6432)) {
+    p.shape = 3;
+    tiles = t6432;
   } else if (count_tiles(m, gs, ng, kShapes[0]) * 2 >= int64_t(cus) * 3) {
     p.shape = 0;
     tiles = count_tiles(m, gs, ng, kShapes[0]);
@@ -533,6 +539,7 @@ extern "C" int wkv7_proj_grouped(int64_t m, const wkv7_proj_group* groups, int32
   hipStream_t s = as_stream(stream);
   if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
   if (p.shape == 2) return launch<128, 64, 3, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  if (p.shape == 3) return launch<64, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
   return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
 }
 
@@ -555,5 +562,6 @@ extern "C" int wkv7_proj_grouped_noalloc(int64_t m, const wkv7_proj_group* group
   hipStream_t s = as_stream(stream);
   if (p.shape == 0) return launch<64, 64, 2, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
   if (p.shape == 2) return launch<128, 64, 3, 2, 4, 128>(m, groups, ngroups, p.parts, ws, s);
+  if (p.shape == 3) return launch<64, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
   return launch<32, 32, 4, 2, 2, 128>(m, groups, ngroups, p.parts, ws, s);
 }
