@@ -1,6 +1,8 @@
 // Varlen WKV7 prefill over slot states: the whole-head kernel (one workgroup
 // of 16 waves per (sequence, head)) and the C entry points. The algorithm,
 // schedule and layouts are described in wkv7_prefill_core.h.
+#include <atomic>
+
 #include "wkv7_prefill_core.h"
 
 namespace wkv7 {
@@ -155,18 +157,19 @@ __global__ __launch_bounds__(kThreads) void prefill_chunked_kernel(
 using namespace wkv7;
 
 namespace {
-// Compute units of the current device (cached per device; 256 on MI355X).
+// Compute units of the current device (cached per device; 256 on MI355X; 0
+// when the runtime cannot say, which keeps one workgroup per (sequence, head)).
 int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 int prefill_launch(float* wkv_layer, int64_t num_rows, int32_t H, const int32_t* slot_ids,
