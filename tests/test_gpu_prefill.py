@@ -287,12 +287,15 @@ def test_prefill_into_rows_and_in_place(dev):
         ops.wkv7_prefill_into(same, same, cu, *vecs, in_ids=[0, 1, 2, 3], out_ids=[1, 2, 3, 4])
 
 
-def test_rejected_device_slot_ids_zero_the_prefill_y(dev):
+@pytest.mark.parametrize("H", [2, 64])
+def test_rejected_device_slot_ids_zero_the_prefill_y(dev, H):
     """A device slot id the kernel's bounds check rejects leaves that
     sequence's state untouched and writes y = 0 for its tokens (as the decode
     step does), so a caller's uninitialised output never leaks; the other
-    sequences are unaffected. Same for wkv7_prefill_into's in and out ids."""
-    H, S = 2, 6
+    sequences are unaffected. Same for wkv7_prefill_into's in and out ids.
+    H = 2 runs the quarter-head kernel (few busy heads), H = 64 the
+    whole-head one."""
+    S = 6
     lens = [40, 100, 17]
     cu = [0, 40, 140, 157]
     gen = synthetic.make_generator(309)
@@ -498,14 +501,16 @@ def test_large_batch_uses_the_64bit_input_path(dev, H):
     assert torch.equal(gpool[[0, 1, 4]].cpu(), pool[[0, 1, 4]])
 
 
+@pytest.mark.parametrize("H", [2, 72])
 @pytest.mark.parametrize("pattern", ["channels", "tokens", "all_max", "limit"])
-def test_decay_extremes_and_scale(dev, pattern):
+def test_decay_extremes_and_scale(dev, pattern, H):
     """RWKV-7's log-decay lies in (-exp(-0.5), 0]. Both ends of that range
     (no decay, and the strongest decay, whose 16-token products reach
     e^{+-9.7} inside a sub-chunk) against the oracle, with scale = 1/8:
     per key channel, per token, or the strongest decay everywhere; and the
-    documented limit of the chunked form, w = -5 everywhere (e^{+-80})."""
-    H, S = 2, 6
+    documented limit of the chunked form, w = -5 everywhere (e^{+-80}).
+    H = 2 runs the quarter-head kernel, H = 72 the whole-head one."""
+    S = 6
     lens = [300, 333]
     cu = np.concatenate([[0], np.cumsum(lens)])
     T = int(cu[-1])
