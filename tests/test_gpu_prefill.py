@@ -676,3 +676,47 @@ def test_runner_prefill_matches_oracle(dev, chunk, segments):
         print(f"layer {layer}: state rel L2 {eh:.2e}, y {ey:.2e}")
         assert eh <= REL_L2 and ey <= REL_L2
     assert torch.equal(bank.wkv[:, [0, 1, 2, 4]].cpu(), before[:, [0, 1, 2, 4]])
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_cached_offsets_under_graph_capture(dev):
+    """Host offsets are uploaded once and cached per (device, offsets). A
+    launch captured in a HIP graph reads the cached copy on every replay, so
+    that copy must outlive the cache's eviction of it; offsets that are not
+    cached yet cannot be uploaded under capture and raise before any launch
+    is recorded. Every replay (with eager launches of other offsets between,
+    which evict the entry) equals the eager result."""
+    H, S = 4, 8
+    lens = [37, 200, 5]
+    cu = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    gen = synthetic.make_generator(101)
+    pool0 = synthetic.initial_states((S + 1, H, 64, 64), gen).to(dev)
+    xs = [x.to(dev) for x in synthetic.order(synthetic.wkv7_vectors((cu[-1], H, 64), gen))]
+    ids = torch.tensor([2, 5, 7], dtype=torch.int32, device=dev)
+    y = torch.empty((cu[-1], H, 64), dtype=torch.bfloat16, device=dev)
+    pool = pool0.clone()
+    ops.wkv7_prefill_varlen(pool, ids, cu, *xs, out=y)  # caches the plan of `cu`
+    torch.cuda.synchronize()
+    ref_y, ref_pool = y.clone(), pool.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.wkv7_prefill_varlen(pool, ids, cu, *xs, out=y)
+    other = [0, 1, 2, 3]  # a one-token-per-sequence batch over slots 1..3
+    for rep in range(3):
+        # more distinct offsets than the cache holds: the captured entry is evicted
+        for n in range(ops._PLAN_CACHE_SIZE + 8):
+            ops._device_plan([0, 1000 + n, 2000 + 1000 * rep + n], dev)
+        pool.copy_(pool0)
+        y.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref_y), f"replay {rep}: y differs"
+        assert torch.equal(pool, ref_pool), f"replay {rep}: state differs"
+        # eager work between replays on the same tensors
+        tmp = pool0.clone()
+        ops.wkv7_prefill_varlen(tmp, [1, 2, 3], other, *(x[:3] for x in xs))
+    g2 = torch.cuda.CUDAGraph()
+    fresh = [0, 11, 12, cu[-1]]
+    with pytest.raises(RuntimeError, match="graph capture"):
+        with torch.cuda.graph(g2):
+            ops.wkv7_prefill_varlen(pool, ids, fresh, *xs, out=y)

@@ -23,6 +23,7 @@ Error behaviour mirrors the reference: invalid arguments raise ``ValueError``
 
 from __future__ import annotations
 
+import threading
 from collections import OrderedDict
 from typing import Iterable, Sequence
 
@@ -263,6 +264,9 @@ def _host_cu(cu, T: int) -> list[int]:
 
 _PLANS: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
 _PLAN_CACHE_SIZE = 256
+_PLANS_LOCK = threading.Lock()
+# plans a HIP graph captured: a replay reads them, so they are never evicted
+_CAPTURED_PLANS: dict[tuple, torch.Tensor] = {}
 
 
 def _device_plan(lst: list[int], dev: torch.device) -> torch.Tensor:
@@ -271,16 +275,36 @@ def _device_plan(lst: list[int], dev: torch.device) -> torch.Tensor:
     repeat the same offsets on every call (one request per call in fixed
     prefill_chunk slices, wkvm/runner/runner.py:52-61), and the upload is the
     largest part of such a call's host time. The tensor is complete when it
-    is returned (a blocking copy from pageable memory) and only ever read."""
+    is returned (a blocking copy from pageable memory) and only ever read;
+    each use is recorded on the caller's stream, so an entry evicted while a
+    launch on another stream still reads it is not reused before that launch
+    ends. A plan used under HIP-graph capture (it must be cached before the
+    capture: the upload cannot be captured) stays alive for good, since the
+    graph's replays read it. The cache is shared by the threads of the
+    process."""
     key = (dev.index, tuple(lst))
-    plan = _PLANS.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
+    with _PLANS_LOCK:
+        plan = _CAPTURED_PLANS.get(key)
+        if plan is None:
+            plan = _PLANS.get(key)
+            if plan is not None:
+                _PLANS.move_to_end(key)
     if plan is None:
+        if capturing:
+            raise RuntimeError("cu_seqlens given as host offsets under graph capture: run the "
+                               "call once before the capture (its device plan is then cached) "
+                               "or pass device cu_seqlens and seq_order")
         plan = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
-        _PLANS[key] = plan
-        if len(_PLANS) > _PLAN_CACHE_SIZE:
-            _PLANS.popitem(last=False)
+        with _PLANS_LOCK:
+            plan = _PLANS.setdefault(key, plan)
+            if len(_PLANS) > _PLAN_CACHE_SIZE:
+                _PLANS.popitem(last=False)
+    if capturing:
+        with _PLANS_LOCK:
+            _CAPTURED_PLANS[key] = plan
     else:
-        _PLANS.move_to_end(key)
+        plan.record_stream(torch.cuda.current_stream(dev))
     return plan
 
 
