@@ -13,12 +13,14 @@ namespace {
 // scores, 12-15 inverse, part = w % 4, one wave of each role per SIMD.
 // Quarter heads (prefill_quarter_kernel: each of four workgroups owns value columns
 // [16 q, 16 q + 16) of the head and repeats the operand, score and inverse
-// work): one state wave, the other roles spread so each SIMD issues about the
-// same (instructions per tick: SIMD 0 state + L_ab + T part 0 ~313; SIMD 1
-// operands 0, 1 + L_ak ~308; SIMD 2 operands 2 + M_rb + T parts 1, 2 ~318;
-// SIMD 3 operands 3 + M_rk + T part 3 ~253), against ~466 for a whole head.
-// Packed 4 bits per wave.
-constexpr uint64_t kQuarterRoles = 0x4344'3323'2212'1110ull;  // wave 15 .. wave 0
+// work): the one state wave has SIMD 0 to itself, since its dependent chain
+// sets the tick here, and the other roles share SIMDs 1-3 (instructions per
+// tick: SIMD 0 state ~203; SIMD 1 operands 0, 1 + L_ak + L_ab ~365; SIMD 2
+// operands 2 + M_rb + T parts 1, 2 ~320; SIMD 3 operands 3 + M_rk + T parts
+// 3, 0 ~320), against ~466 for a whole head. (The state wave beside L_ab and
+// T part 0 on SIMD 0 was 1.7 % slower per 512-token launch.) Packed 4 bits
+// per wave.
+constexpr uint64_t kQuarterRoles = 0x3324'3324'2214'1110ull;  // wave 15 .. wave 0
 constexpr uint64_t kQuarterParts = 0x0200'3110'3210'3200ull;
 
 template <bool kF32Out, bool kBuf, bool kScaled>

@@ -36,8 +36,16 @@ from .layout import HEAD_SIZE
 _IDS = (list, tuple, range, np.ndarray)
 
 
+# The current stream's raw handle: torch's own fast accessor when present (a
+# launch wrapper pays for torch.cuda.current_stream's Stream object otherwise).
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    if _RAW_STREAM is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _RAW_STREAM(idx)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -112,7 +120,8 @@ def _check_vectors(xs: Sequence[torch.Tensor], shape: tuple[int, ...], device: t
                    what: str) -> list[torch.Tensor]:
     out = []
     for name, x in zip("rwkvab", xs):
-        _require_cuda(x, f"{what}.{name}")
+        if not (isinstance(x, torch.Tensor) and x.is_cuda):  # (message built on failure only)
+            _require_cuda(x, f"{what}.{name}")
         if x.dtype != torch.bfloat16:
             raise ValueError(f"{what}.{name} must be bfloat16, got {x.dtype}")
         if tuple(x.shape) != shape:
@@ -262,11 +271,11 @@ def _host_cu(cu, T: int) -> list[int]:
     return lst
 
 
-_PLANS: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_PLANS: "OrderedDict[tuple, tuple[torch.Tensor, int]]" = OrderedDict()  # (plan, its stream)
 _PLAN_CACHE_SIZE = 256
 _PLANS_LOCK = threading.Lock()
 # plans a HIP graph captured: a replay reads them, so they are never evicted
-_CAPTURED_PLANS: dict[tuple, torch.Tensor] = {}
+_CAPTURED_PLANS: dict[tuple, tuple[torch.Tensor, int]] = {}
 
 
 def _device_plan(lst: list[int], dev: torch.device) -> torch.Tensor:
@@ -275,35 +284,37 @@ def _device_plan(lst: list[int], dev: torch.device) -> torch.Tensor:
     repeat the same offsets on every call (one request per call in fixed
     prefill_chunk slices, wkvm/runner/runner.py:52-61), and the upload is the
     largest part of such a call's host time. The tensor is complete when it
-    is returned (a blocking copy from pageable memory) and only ever read;
-    each use is recorded on the caller's stream, so an entry evicted while a
-    launch on another stream still reads it is not reused before that launch
-    ends. A plan used under HIP-graph capture (it must be cached before the
-    capture: the upload cannot be captured) stays alive for good, since the
-    graph's replays read it. The cache is shared by the threads of the
-    process."""
+    is returned (a blocking copy from pageable memory) and only ever read; a
+    use on another stream than the one it was made on is recorded on that
+    stream, so an entry evicted while such a launch still reads it is not
+    reused before the launch ends. A plan used under HIP-graph capture (it
+    must be cached before the capture: the upload cannot be captured) stays
+    alive for good, since the graph's replays read it. The cache is shared by
+    the threads of the process."""
     key = (dev.index, tuple(lst))
     capturing = torch.cuda.is_current_stream_capturing()
+    stream = _stream_ptr(dev)
     with _PLANS_LOCK:
-        plan = _CAPTURED_PLANS.get(key)
-        if plan is None:
-            plan = _PLANS.get(key)
-            if plan is not None:
+        entry = _CAPTURED_PLANS.get(key)
+        if entry is None:
+            entry = _PLANS.get(key)
+            if entry is not None:
                 _PLANS.move_to_end(key)
-    if plan is None:
+    if entry is None:
         if capturing:
             raise RuntimeError("cu_seqlens given as host offsets under graph capture: run the "
                                "call once before the capture (its device plan is then cached) "
                                "or pass device cu_seqlens and seq_order")
         plan = torch.tensor(lst + longest_first(lst), dtype=torch.int32, device=dev)
         with _PLANS_LOCK:
-            plan = _PLANS.setdefault(key, plan)
+            entry = _PLANS.setdefault(key, (plan, stream))
             if len(_PLANS) > _PLAN_CACHE_SIZE:
                 _PLANS.popitem(last=False)
+    plan, made_on = entry
     if capturing:
         with _PLANS_LOCK:
-            _CAPTURED_PLANS[key] = plan
-    else:
+            _CAPTURED_PLANS[key] = entry
+    elif stream != made_on:
         plan.record_stream(torch.cuda.current_stream(dev))
     return plan
 
